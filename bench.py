@@ -1,0 +1,261 @@
+"""Benchmark of the fused stochastic-rounding AdamW step on one MI355X.
+
+``python bench.py [--steps K] [--warmup W] [--workload NAME]`` times K
+optimizer steps (one ``AdamWHip.step()`` = one pass of the fused kernel over
+every parameter) after W untimed warmup steps, and prints ONE JSON line.
+
+Default workload ``north_star``: AdamW with stochastically rounded BF16
+moments over the 1.55 G-element multi-tensor set of BASELINE config 4's
+shapes (7 blocks of 4x 4096x4096 + 3x 4096x11008, plus a 32000x4096
+embedding; FP32 parameters and gradients), lr=3e-4, betas=(0.9, 0.999),
+eps=1e-8, weight_decay=0.01, seed=7.  Inputs are synthetic (seeded normal
+draws generated on the GPU), resident in HBM before timing starts.
+
+Roofline: the kernel is HBM-bound.  Algorithmic bytes per element are the
+minimum reads+writes: parameter read+write, gradient read, each moment
+read+write, at their storage widths (20 B for FP32 p/g and BF16 moments).
+``achieved`` = bytes per launch / mean kernel time from HIP events around
+each step on the launch stream (one launch per step).  ``traffic`` comes
+from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE measurement of the same
+workload, scaled by a copy-kernel calibration, when present.
+
+cpu_baseline: the reference's eager CPU path (restated in oracle/sr_oracle.py
+with the same torch operations) timed on this host on a bounded sample of
+the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "stochastic-rounding-pytorch_amd"))
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+
+C4_BLOCK = [(4096, 4096)] * 4 + [(4096, 11008)] * 3
+WORKLOADS = {
+    # name: (optimizer, shapes, param dtype, grad dtype, state formats, hyperparameters)
+    "north_star": dict(
+        optimizer="adamw",
+        shapes=C4_BLOCK * 7 + [(32000, 4096)],
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=((torch.bfloat16, "stochastic"), (torch.bfloat16, "stochastic")),
+        grad_std=1e-3,
+        hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
+        seed=7,
+    ),
+    "c2_single_2e26": dict(
+        optimizer="adamw",
+        shapes=[(1 << 26,)],
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=((torch.bfloat16, "stochastic"), (torch.bfloat16, "stochastic")),
+        grad_std=1e-3,
+        hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
+        seed=7,
+    ),
+    "c4_fp8_mixed": dict(
+        optimizer="adamw",
+        shapes=C4_BLOCK * 7 + [(32000, 4096)],
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=((torch.float8_e4m3fn, "stochastic"), (torch.bfloat16, "stochastic")),
+        grad_std=1e-3,
+        hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
+        seed=7,
+    ),
+    "c5_sgdm_fp16": dict(
+        optimizer="sgdm",
+        shapes=[(2048, 2048)] * 256,
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=((torch.float16, "stochastic"),),
+        grad_std=1e-2,
+        hparams=dict(lr=0.1, momentum=0.9),
+        seed=11,
+    ),
+}
+
+
+def bytes_per_element(spec) -> int:
+    size = lambda dt: torch.empty((), dtype=dt).element_size()  # noqa: E731
+    states = sum(2 * size(dt) for dt, _ in spec["formats"])
+    return 2 * size(spec["p_dtype"]) + size(spec["g_dtype"]) + states
+
+
+class _Param(torch.nn.Parameter):
+    """Parameter whose gradient may have another dtype (BF16 grads of FP32 params)."""
+
+    @property
+    def grad(self):
+        return getattr(self, "_gradient", None)
+
+    @grad.setter
+    def grad(self, value):
+        self._gradient = value
+
+
+def build(spec, device):
+    import sr_states
+    from sr_states import StateFormat
+
+    gen = torch.Generator(device=device).manual_seed(spec["seed"])
+    params = []
+    for shape in spec["shapes"]:
+        p = _Param(torch.empty(shape, device=device, dtype=spec["p_dtype"]))
+        with torch.no_grad():
+            p.normal_(std=0.02, generator=gen)
+        g = torch.empty(shape, device=device, dtype=torch.float32).normal_(std=spec["grad_std"], generator=gen)
+        p.grad = g.to(spec["g_dtype"])
+        params.append(p)
+    names = ("exp_avg", "exp_avg_sq") if spec["optimizer"] == "adamw" else ("momentum_buffer",)
+    formats = {n: StateFormat(d, r) for n, (d, r) in zip(names, spec["formats"])}
+    if spec["optimizer"] == "adamw":
+        opt = sr_states.AdamWHip(params, state_format=formats, seed=spec["seed"], **spec["hparams"])
+    else:
+        opt = sr_states.SGDMHip(params, state_format=formats, seed=spec["seed"], **spec["hparams"])
+    return params, opt
+
+
+def cpu_baseline(spec, target_seconds: float = 12.0):
+    """Time the eager CPU path (oracle restatement) on one tensor of the workload."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import sr_oracle
+
+    shape = max(spec["shapes"], key=lambda s: math.prod(s))
+    n = min(math.prod(shape), 1 << 24)
+    gen = torch.Generator().manual_seed(spec["seed"])
+    p = (torch.randn(n, generator=gen) * 0.02).to(spec["p_dtype"])
+    g = (torch.randn(n, generator=gen) * spec["grad_std"]).to(spec["g_dtype"])
+    formats = tuple(sr_oracle.Fmt(d, r) for d, r in spec["formats"])
+    group = {"params": [p], "grads": [g], "formats": formats, "sr_seed": spec["seed"], **spec["hparams"]}
+    cls = sr_oracle.AdamWOracle if spec["optimizer"] == "adamw" else sr_oracle.SGDMOracle
+    opt = cls([group])
+    opt.step()  # allocate states
+    times = []
+    start = time.perf_counter()
+    while time.perf_counter() - start < target_seconds or len(times) < 3:
+        t0 = time.perf_counter_ns()
+        opt.step()
+        times.append((time.perf_counter_ns() - t0) / 1e9)
+    median = sorted(times)[len(times) // 2]
+    return {
+        "value": n / median,
+        "unit": "params/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{len(times)} eager steps of one {n}-element tensor of the workload "
+        f"(torch {torch.__version__}, {torch.backends.cpu.get_cpu_capability()}, "
+        f"{os.cpu_count()} host CPUs visible), median step {median * 1e3:.1f} ms",
+    }
+
+
+def load_traffic(workload: str, bytes_per_launch: float):
+    path = ROOT / "profiles" / f"traffic_{workload}.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    return data.get("hbm_bytes_per_launch")
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="north_star")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        raise SystemExit(
+            "bench.py measures one GPU: the fused update needs no collective, and each rank "
+            "would run this same kernel on its own shard; run with --gpus 1"
+        )
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    spec = WORKLOADS[args.workload]
+    device = torch.device("cuda", 0)
+    params, opt = build(spec, device)
+    elements = sum(p.numel() for p in params)
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    total_start = torch.cuda.Event(enable_timing=True)
+    total_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    total_start.record()
+    for i in range(args.steps):
+        starts[i].record()
+        opt.step()
+        ends[i].record()
+    total_end.record()
+    torch.cuda.synchronize()
+    total_ms = total_start.elapsed_time(total_end)
+    kernel_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / args.steps
+    ms_per_step = total_ms / args.steps
+
+    bpe = bytes_per_element(spec)
+    bytes_per_launch = bpe * elements
+    achieved = bytes_per_launch / (kernel_ms / 1e3) / 1e9
+    traffic = load_traffic(args.workload, bytes_per_launch)
+    dtype = "f32"
+    result = {
+        "metric": "AdamW-SR step: params updated/sec and achieved HBM GB/s (% of peak), 1 MI355X"
+        if spec["optimizer"] == "adamw" else "SGDM-SR step: params updated/sec, 1 MI355X",
+        "value": elements / (ms_per_step / 1e3),
+        "unit": "params/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic (seeded normal draws on the GPU)",
+        "config": {
+            "workload": args.workload,
+            "optimizer": spec["optimizer"],
+            "elements": elements,
+            "tensors": len(spec["shapes"]),
+            "param_dtype": str(spec["p_dtype"]).replace("torch.", ""),
+            "grad_dtype": str(spec["g_dtype"]).replace("torch.", ""),
+            "state_formats": [f"{str(d).replace('torch.', '')}/{r}" for d, r in spec["formats"]],
+            "bytes_per_element": bpe,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBPS,
+            "traffic": traffic,
+            "kernel_ms": kernel_ms,
+            "algorithmic_bytes_per_launch": bytes_per_launch,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        del params, opt
+        torch.cuda.empty_cache()
+        result["cpu_baseline"] = cpu_baseline(spec, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,169 @@
+/*
+ * sr_states_hip.h -- C ABI of the MI355X (gfx950) backend for sr_states.
+ *
+ * This is the drop-in boundary for the fused stochastic-rounding optimizer
+ * step and the standalone cast.  Every entry point takes plain device
+ * pointers, element counts, scalars and a HIP stream handle; no torch types
+ * cross the boundary.  Each declaration names the reference interface it
+ * replaces (paths relative to the reference repository root).
+ *
+ * Conventions
+ *   - Return value: 0 on success, otherwise a nonzero SR_ERR_* code.  The
+ *     message for the most recent failure on the calling thread is returned
+ *     by sr_last_error().
+ *   - `stream` is a hipStream_t passed as void* (0 = the null stream).  All
+ *     launches are asynchronous on that stream; nothing synchronizes.
+ *   - Pointers are borrowed for the duration of the launch; the caller keeps
+ *     the memory alive until the stream has consumed it.
+ *   - Counters are 32-bit: every seed/offset/step word is taken modulo 2^32,
+ *     exactly as the reference masks them (sr_states/_hash.py:5-50).
+ */
+#ifndef SR_STATES_HIP_H
+#define SR_STATES_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SR_ABI_VERSION 1
+
+/* Storage dtypes (torch.float32, bfloat16, float16, float8_e4m3fn,
+ * float8_e5m2).  The set mirrors the built-in rounding table of the
+ * reference (sr_states/rounding.py:135-142). */
+enum sr_dtype {
+  SR_F32 = 0,
+  SR_BF16 = 1,
+  SR_F16 = 2,
+  SR_E4M3 = 3,
+  SR_E5M2 = 4
+};
+
+/* Rounding rules ("nearest", "stochastic"); FP32 ignores the rule, as the
+ * reference maps both FP32 rules to the identity (sr_states/rounding.py:135-136). */
+enum sr_rule {
+  SR_NEAREST = 0,
+  SR_STOCHASTIC = 1
+};
+
+enum sr_error {
+  SR_OK = 0,
+  SR_ERR_ARGUMENT = 1,   /* invalid dtype / rule / size / block size */
+  SR_ERR_HIP = 2,        /* a HIP runtime call failed (message has details) */
+  SR_ERR_UNSUPPORTED = 3 /* combination not compiled into this library */
+};
+
+/* Elements handled by one thread per tile; a tile is block_size * this many
+ * elements.  Hosts use it to lay out the tile ranges of sr_row tables. */
+#define SR_ELEMENTS_PER_THREAD 8
+
+/* Row flag: every pointer of the row is 16-byte aligned, so full tiles take
+ * the 128-bit vector path.  Rows without it take the coalesced scalar path. */
+#define SR_ROW_VECTOR 1u
+/* Row flag: `param_index` already holds the update key (functional API);
+ * the kernel then skips the on-device key derivation. */
+#define SR_ROW_KEYED 2u
+
+/* One parameter of a multi-tensor bucket (64 bytes, device memory).
+ * Replaces the reference's three tables `meta`, `chunks`, `pointers`
+ * (sr_states/triton/_multi_tensor.py:146-239, consumed by
+ * sr_states/triton/_common.py:47-60). */
+typedef struct sr_row {
+  uint64_t ptr[4];      /* parameter, gradient, state 0, state 1 (0 for SGDM) */
+  int64_t numel;        /* elements of this parameter (>= 1) */
+  uint32_t tile_begin;  /* first tile of this row in the bucket's tile space */
+  uint32_t tile_end;    /* one past its last tile; tiles are contiguous */
+  uint32_t param_index; /* global parameter index, or the key if SR_ROW_KEYED */
+  uint32_t shard_start; /* flat index of the first local element (mod 2^32) */
+  uint32_t flags;       /* SR_ROW_* */
+  uint32_t reserved;
+} sr_row;
+
+/* AdamW launch scalars, already rounded to FP32 by the host exactly as the
+ * eager reference rounds its Python-double scalars
+ * (sr_states/reference/adamw.py:86-96; triton/adamw.py:224-234). */
+typedef struct sr_adamw_hparams {
+  float beta1;            /* f32(beta1) */
+  float beta2;            /* f32(beta2) */
+  float one_minus_beta1;  /* f32(1 - beta1) */
+  float one_minus_beta2;  /* f32(1 - beta2) */
+  float neg_step_size;    /* f32(-lr / (1 - beta1^step)) */
+  float correction2_sqrt; /* f32(sqrt(1 - beta2^step)) */
+  float decay;            /* f32(1 - lr * weight_decay) */
+  float eps;              /* f32(eps) */
+} sr_adamw_hparams;
+
+/* Momentum-SGD launch scalars (sr_states/reference/sgd.py:62-64). */
+typedef struct sr_sgdm_hparams {
+  float momentum; /* f32(momentum_factor) */
+  float neg_lr;   /* f32(-lr) */
+} sr_sgdm_hparams;
+
+/* ---- library ---------------------------------------------------------- */
+
+/* Returns SR_ABI_VERSION. */
+int sr_abi_version(void);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* sr_last_error(void);
+
+/* ---- counter-hash keys (host) ----------------------------------------- */
+
+/* Replaces sr_states/_hash.py:18-23 `update_key(seed, step, param_index)`;
+ * seed and step are their low 64 bits (two's complement). */
+uint32_t sr_update_key(uint64_t seed, uint64_t step, uint32_t param_index);
+
+/* Replaces sr_states/_hash.py:26-28 `state_key(key, state_index)`. */
+uint32_t sr_state_key(uint32_t key, uint32_t state_index);
+
+/* ---- standalone cast -------------------------------------------------- */
+
+/* y[i] = round(x[i]) for i < n, counter = i + seed + offset (mod 2^32).
+ * x: contiguous FP32; y: contiguous storage of `dtype`; x and y disjoint.
+ * Replaces the `_cast_kernel` launch of sr_states/triton/cast.py:47-60 and
+ * `_sr_cast_bf16_kernel` of sr_states/triton/sr_cast.py:191-224; its
+ * arithmetic is sr_states/rounding.py:97-142. */
+int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule,
+            uint32_t seed, uint32_t offset, int block_size, void* stream);
+
+/* ---- fused AdamW ------------------------------------------------------ */
+
+/* One tensor.  p, g: FP32 or BF16; m, v: any sr_dtype.  `key` is the
+ * parameter's update key; `offset` the flat shard start.
+ * Replaces `_fused_adamw_kernel` (sr_states/triton/adamw.py:160-221). */
+int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n,
+                  int p_dtype, int g_dtype, int m_dtype, int m_rule,
+                  int v_dtype, int v_rule, const sr_adamw_hparams* hp,
+                  uint32_t key, uint32_t offset, int block_size, void* stream);
+
+/* One bucket: `rows` is a device table of nrows sr_row records whose tile
+ * ranges cover [0, total_tiles) in order.  Keys are derived on the device
+ * from (seed, rng_step, param_index).
+ * Replaces `_multi_adamw_kernel` and its launch
+ * (sr_states/triton/adamw.py:102-157, 289-319). */
+int sr_adamw_multi(const sr_row* rows, int nrows, uint32_t total_tiles,
+                   int p_dtype, int g_dtype, int m_dtype, int m_rule,
+                   int v_dtype, int v_rule, const sr_adamw_hparams* hp,
+                   uint64_t seed, uint64_t rng_step, int block_size, void* stream);
+
+/* ---- fused momentum SGD ----------------------------------------------- */
+
+/* Replaces `_fused_sgdm_kernel` (sr_states/triton/sgd.py:434-490). */
+int sr_sgdm_step(void* p, const void* g, void* u, int64_t n,
+                 int p_dtype, int g_dtype, int u_dtype, int u_rule,
+                 const sr_sgdm_hparams* hp, uint32_t key, uint32_t offset,
+                 int block_size, void* stream);
+
+/* Replaces `_multi_sgdm_kernel` and its launch
+ * (sr_states/triton/sgd.py:393-431, 533-556). */
+int sr_sgdm_multi(const sr_row* rows, int nrows, uint32_t total_tiles,
+                  int p_dtype, int g_dtype, int u_dtype, int u_rule,
+                  const sr_sgdm_hparams* hp, uint64_t seed, uint64_t rng_step,
+                  int block_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SR_STATES_HIP_H */

@@ -1,0 +1,97 @@
+"""Compile the gfx950 kernels and the C ABI into sr_states/libsr_states_hip.so.
+
+Run ``python build.py`` from anywhere.  The AdamW instantiations are split
+into nine translation units (one per first-moment encoding) that compile in
+parallel; the shared library is linked in place next to the Python package,
+so it travels with the source tree.
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+CSRC = ROOT / "csrc"
+BUILD = ROOT / "_build"
+OUTPUT = ROOT / "sr_states" / "libsr_states_hip.so"
+ARCH = "gfx950"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# -ffp-contract=off: only the explicit fmaf() calls may fuse, matching the
+# eager CPU reference.  Division and sqrt stay IEEE correctly rounded.
+# Packed FP32 instructions are disabled on this platform.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-mcode-object-version=5",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def units() -> list[tuple[Path, list[str], Path]]:
+    jobs = [(CSRC / "sr_abi.hip", [], BUILD / "sr_abi.o")]
+    jobs.append((CSRC / "sr_sgdm_cast.hip", [], BUILD / "sr_sgdm_cast.o"))
+    for enc in range(9):
+        jobs.append((CSRC / "sr_adamw.hip", [f"-DSR_M_ENC={enc}"], BUILD / f"sr_adamw_m{enc}.o"))
+    return jobs
+
+
+def _run(cmd: list[str]) -> None:
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"command failed ({result.returncode}): {' '.join(cmd)}\n{result.stderr}")
+    noise = "not a recognized feature for this target"
+    for line in result.stderr.splitlines():
+        if line.strip() and noise not in line:
+            print(line, file=sys.stderr)
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every unit and link the shared library; returns its path."""
+    if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    BUILD.mkdir(exist_ok=True)
+    commands = [
+        [HIPCC, *HIP_FLAGS, *defines, "-c", str(src), "-o", str(obj)]
+        for src, defines, obj in units()
+    ]
+    workers = jobs or min(len(commands), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(workers) as pool:
+        for cmd, _ in zip(commands, pool.map(_run, commands)):
+            if verbose:
+                print(" ".join(cmd))
+    tmp = OUTPUT.with_suffix(".so.tmp")
+    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp)]
+    link += [str(obj) for _, _, obj in units()]
+    _run(link)
+    os.replace(tmp, OUTPUT)
+    return OUTPUT
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("-j", "--jobs", type=int, default=None)
+    parser.add_argument("-v", "--verbose", action="store_true")
+    args = parser.parse_args()
+    path = build(args.jobs, args.verbose)
+    print(path)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,284 @@
+// sr_abi.hip -- extern "C" entry points of libsr_states_hip.so.
+//
+// Validation of dtypes, rules, sizes and launch shapes happens here; the
+// Python layer validates tensors, layouts and hyperparameters before it
+// calls in.  Launches go through hipLaunchKernel with the kernel's host stub
+// so that instantiations can live in separately compiled units.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+
+#include "../../include/sr_states_hip.h"
+#include "sr_kernels.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t err, const char* what) {
+  return fail(SR_ERR_HIP, "%s failed: %s (%d)", what, hipGetErrorString(err), static_cast<int>(err));
+}
+
+struct Tables {
+  sr::KernelTableAdamW adamw{};
+  sr::KernelTableSgdm sgdm{};
+  sr::KernelTableCast cast{};
+};
+
+const Tables& tables() {
+  static const Tables t = [] {
+    Tables r{};
+    sr::register_adamw_m0(r.adamw);
+    sr::register_adamw_m1(r.adamw);
+    sr::register_adamw_m2(r.adamw);
+    sr::register_adamw_m3(r.adamw);
+    sr::register_adamw_m4(r.adamw);
+    sr::register_adamw_m5(r.adamw);
+    sr::register_adamw_m6(r.adamw);
+    sr::register_adamw_m7(r.adamw);
+    sr::register_adamw_m8(r.adamw);
+    sr::register_sgdm(r.sgdm);
+    sr::register_cast(r.cast);
+    return r;
+  }();
+  return t;
+}
+
+// (dtype, rule) -> storage encoding index, or -1.
+int state_enc(int dtype, int rule) {
+  if (rule != SR_NEAREST && rule != SR_STOCHASTIC) return -1;
+  switch (dtype) {
+    case SR_F32: return sr::ENC_F32;
+    case SR_BF16: return rule == SR_STOCHASTIC ? sr::ENC_BF16_SR : sr::ENC_BF16_RN;
+    case SR_F16: return rule == SR_STOCHASTIC ? sr::ENC_F16_SR : sr::ENC_F16_RN;
+    case SR_E4M3: return rule == SR_STOCHASTIC ? sr::ENC_E4M3_SR : sr::ENC_E4M3_RN;
+    case SR_E5M2: return rule == SR_STOCHASTIC ? sr::ENC_E5M2_SR : sr::ENC_E5M2_RN;
+    default: return -1;
+  }
+}
+
+// Parameter / gradient storage -> table index (FP32 0, BF16 1), or -1.
+int pg_index(int dtype) { return dtype == SR_F32 ? 0 : (dtype == SR_BF16 ? 1 : -1); }
+
+bool valid_block(int block) { return block >= 64 && block <= sr::kMaxBlock && block % 64 == 0; }
+
+// Persistent grid: as many workgroups as fit on the device at once, capped by
+// the number of tiles.  Occupancy is queried once per (device, kernel,
+// block, LDS bytes).
+int grid_size(const void* fn, int block, size_t lds, uint32_t tiles, unsigned* grid) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, const void*, int, size_t>, unsigned> cache;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+  const auto key = std::make_tuple(dev, fn, block, lds);
+  unsigned resident = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) resident = it->second;
+  }
+  if (!resident) {
+    int cus = 0, per_cu = 0;
+    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return hip_fail(err, "hipDeviceGetAttribute");
+    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, lds);
+    if (err != hipSuccess) return hip_fail(err, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    if (cus <= 0 || per_cu <= 0) return fail(SR_ERR_HIP, "kernel cannot be resident (block %d)", block);
+    resident = static_cast<unsigned>(cus) * static_cast<unsigned>(per_cu);
+    std::lock_guard<std::mutex> lock(mu);
+    cache[key] = resident;
+  }
+  *grid = tiles < resident ? tiles : resident;
+  return SR_OK;
+}
+
+int launch(const void* fn, int block, size_t lds, uint32_t tiles, void* arg, void* stream) {
+  unsigned grid = 0;
+  if (int rc = grid_size(fn, block, lds, tiles, &grid)) return rc;
+  void* args[] = {arg};
+  hipError_t err = hipLaunchKernel(fn, dim3(grid), dim3(block), args, lds,
+                                   static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return hip_fail(err, "hipLaunchKernel");
+  return SR_OK;
+}
+
+// Tiles covering n elements, or fail if they do not fit 32-bit tile indices.
+int tiles_for(int64_t n, int block, uint32_t* tiles) {
+  const int64_t tile = static_cast<int64_t>(block) * sr::kVec;
+  const int64_t count = (n + tile - 1) / tile;
+  if (count > 0xFFFFFFFFll) return fail(SR_ERR_ARGUMENT, "%lld elements exceed the tile index range", (long long)n);
+  *tiles = static_cast<uint32_t>(count);
+  return SR_OK;
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+sr::AdamWScalars adamw_scalars(const sr_adamw_hparams& h) {
+  return {h.beta1, h.beta2, h.one_minus_beta1, h.one_minus_beta2,
+          h.neg_step_size, h.correction2_sqrt, h.decay, h.eps};
+}
+
+}  // namespace
+
+extern "C" {
+
+int sr_abi_version(void) { return SR_ABI_VERSION; }
+
+const char* sr_last_error(void) { return g_error.c_str(); }
+
+uint32_t sr_update_key(uint64_t seed, uint64_t step, uint32_t param_index) {
+  return sr::update_key(static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32),
+                        static_cast<uint32_t>(step), static_cast<uint32_t>(step >> 32), param_index);
+}
+
+uint32_t sr_state_key(uint32_t key, uint32_t state_index) { return sr::state_key(key, state_index); }
+
+int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule, uint32_t seed, uint32_t offset,
+            int block_size, void* stream) {
+  const int enc = state_enc(dtype, rule);
+  if (enc < 0) return fail(SR_ERR_ARGUMENT, "unsupported cast dtype %d / rule %d", dtype, rule);
+  if (!valid_block(block_size)) return fail(SR_ERR_ARGUMENT, "invalid block size %d", block_size);
+  if (n < 0) return fail(SR_ERR_ARGUMENT, "negative element count");
+  if (n == 0) return SR_OK;
+  if (!x || !y) return fail(SR_ERR_ARGUMENT, "null pointer");
+  sr::CastArgs a{};
+  a.x = static_cast<const float*>(x);
+  a.y = y;
+  a.n = n;
+  a.counter_base = seed + offset;
+  a.vector_ok = aligned16(x) && aligned16(y);
+  if (int rc = tiles_for(n, block_size, &a.total_tiles)) return rc;
+  return launch(tables().cast[enc], block_size, 0, a.total_tiles, &a, stream);
+}
+
+int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n, int p_dtype, int g_dtype,
+                  int m_dtype, int m_rule, int v_dtype, int v_rule, const sr_adamw_hparams* hp,
+                  uint32_t key, uint32_t offset, int block_size, void* stream) {
+  const int pi = pg_index(p_dtype), gi = pg_index(g_dtype);
+  const int me = state_enc(m_dtype, m_rule), ve = state_enc(v_dtype, v_rule);
+  if (pi < 0 || gi < 0) return fail(SR_ERR_ARGUMENT, "parameter and gradient must be FP32 or BF16");
+  if (me < 0 || ve < 0) return fail(SR_ERR_ARGUMENT, "unsupported state dtype or rule");
+  if (!valid_block(block_size)) return fail(SR_ERR_ARGUMENT, "invalid block size %d", block_size);
+  if (!hp) return fail(SR_ERR_ARGUMENT, "null hyperparameters");
+  if (n < 0) return fail(SR_ERR_ARGUMENT, "negative element count");
+  if (n == 0) return SR_OK;
+  if (!p || !g || !m || !v) return fail(SR_ERR_ARGUMENT, "null pointer");
+  sr::AdamWArgs a{};
+  a.rows = nullptr;
+  a.nrows = 1;
+  a.s = adamw_scalars(*hp);
+  if (int rc = tiles_for(n, block_size, &a.total_tiles)) return rc;
+  sr_row& r = a.inline_row;
+  r.ptr[0] = reinterpret_cast<uint64_t>(p);
+  r.ptr[1] = reinterpret_cast<uint64_t>(g);
+  r.ptr[2] = reinterpret_cast<uint64_t>(m);
+  r.ptr[3] = reinterpret_cast<uint64_t>(v);
+  r.numel = n;
+  r.tile_begin = 0;
+  r.tile_end = a.total_tiles;
+  r.param_index = key;
+  r.shard_start = offset;
+  r.flags = SR_ROW_KEYED |
+            ((aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v)) ? SR_ROW_VECTOR : 0u);
+  return launch(tables().adamw[pi][gi][me][ve], block_size, sizeof(uint32_t), a.total_tiles, &a,
+                stream);
+}
+
+int sr_adamw_multi(const sr_row* rows, int nrows, uint32_t total_tiles, int p_dtype, int g_dtype,
+                   int m_dtype, int m_rule, int v_dtype, int v_rule, const sr_adamw_hparams* hp,
+                   uint64_t seed, uint64_t rng_step, int block_size, void* stream) {
+  const int pi = pg_index(p_dtype), gi = pg_index(g_dtype);
+  const int me = state_enc(m_dtype, m_rule), ve = state_enc(v_dtype, v_rule);
+  if (pi < 0 || gi < 0) return fail(SR_ERR_ARGUMENT, "parameter and gradient must be FP32 or BF16");
+  if (me < 0 || ve < 0) return fail(SR_ERR_ARGUMENT, "unsupported state dtype or rule");
+  if (!valid_block(block_size)) return fail(SR_ERR_ARGUMENT, "invalid block size %d", block_size);
+  if (!hp || !rows) return fail(SR_ERR_ARGUMENT, "null argument");
+  if (nrows < 1 || nrows > sr::kMaxRows)
+    return fail(SR_ERR_ARGUMENT, "row count %d outside [1, %d]", nrows, sr::kMaxRows);
+  if (total_tiles == 0) return fail(SR_ERR_ARGUMENT, "empty tile range");
+  sr::AdamWArgs a{};
+  a.rows = rows;
+  a.nrows = static_cast<uint32_t>(nrows);
+  a.total_tiles = total_tiles;
+  a.s = adamw_scalars(*hp);
+  a.seed_lo = static_cast<uint32_t>(seed);
+  a.seed_hi = static_cast<uint32_t>(seed >> 32);
+  a.step_lo = static_cast<uint32_t>(rng_step);
+  a.step_hi = static_cast<uint32_t>(rng_step >> 32);
+  return launch(tables().adamw[pi][gi][me][ve], block_size, sizeof(uint32_t) * nrows, total_tiles,
+                &a, stream);
+}
+
+int sr_sgdm_step(void* p, const void* g, void* u, int64_t n, int p_dtype, int g_dtype, int u_dtype,
+                 int u_rule, const sr_sgdm_hparams* hp, uint32_t key, uint32_t offset,
+                 int block_size, void* stream) {
+  const int pi = pg_index(p_dtype), gi = pg_index(g_dtype);
+  const int ue = state_enc(u_dtype, u_rule);
+  if (pi < 0 || gi < 0) return fail(SR_ERR_ARGUMENT, "parameter and gradient must be FP32 or BF16");
+  if (ue < 0) return fail(SR_ERR_ARGUMENT, "unsupported state dtype or rule");
+  if (!valid_block(block_size)) return fail(SR_ERR_ARGUMENT, "invalid block size %d", block_size);
+  if (!hp) return fail(SR_ERR_ARGUMENT, "null hyperparameters");
+  if (n < 0) return fail(SR_ERR_ARGUMENT, "negative element count");
+  if (n == 0) return SR_OK;
+  if (!p || !g || !u) return fail(SR_ERR_ARGUMENT, "null pointer");
+  sr::SgdmArgs a{};
+  a.rows = nullptr;
+  a.nrows = 1;
+  a.s = {hp->momentum, hp->neg_lr};
+  if (int rc = tiles_for(n, block_size, &a.total_tiles)) return rc;
+  sr_row& r = a.inline_row;
+  r.ptr[0] = reinterpret_cast<uint64_t>(p);
+  r.ptr[1] = reinterpret_cast<uint64_t>(g);
+  r.ptr[2] = reinterpret_cast<uint64_t>(u);
+  r.ptr[3] = 0;
+  r.numel = n;
+  r.tile_begin = 0;
+  r.tile_end = a.total_tiles;
+  r.param_index = key;
+  r.shard_start = offset;
+  r.flags = SR_ROW_KEYED | ((aligned16(p) && aligned16(g) && aligned16(u)) ? SR_ROW_VECTOR : 0u);
+  return launch(tables().sgdm[pi][gi][ue], block_size, sizeof(uint32_t), a.total_tiles, &a, stream);
+}
+
+int sr_sgdm_multi(const sr_row* rows, int nrows, uint32_t total_tiles, int p_dtype, int g_dtype,
+                  int u_dtype, int u_rule, const sr_sgdm_hparams* hp, uint64_t seed,
+                  uint64_t rng_step, int block_size, void* stream) {
+  const int pi = pg_index(p_dtype), gi = pg_index(g_dtype);
+  const int ue = state_enc(u_dtype, u_rule);
+  if (pi < 0 || gi < 0) return fail(SR_ERR_ARGUMENT, "parameter and gradient must be FP32 or BF16");
+  if (ue < 0) return fail(SR_ERR_ARGUMENT, "unsupported state dtype or rule");
+  if (!valid_block(block_size)) return fail(SR_ERR_ARGUMENT, "invalid block size %d", block_size);
+  if (!hp || !rows) return fail(SR_ERR_ARGUMENT, "null argument");
+  if (nrows < 1 || nrows > sr::kMaxRows)
+    return fail(SR_ERR_ARGUMENT, "row count %d outside [1, %d]", nrows, sr::kMaxRows);
+  if (total_tiles == 0) return fail(SR_ERR_ARGUMENT, "empty tile range");
+  sr::SgdmArgs a{};
+  a.rows = rows;
+  a.nrows = static_cast<uint32_t>(nrows);
+  a.total_tiles = total_tiles;
+  a.s = {hp->momentum, hp->neg_lr};
+  a.seed_lo = static_cast<uint32_t>(seed);
+  a.seed_hi = static_cast<uint32_t>(seed >> 32);
+  a.step_lo = static_cast<uint32_t>(rng_step);
+  a.step_hi = static_cast<uint32_t>(rng_step >> 32);
+  return launch(tables().sgdm[pi][gi][ue], block_size, sizeof(uint32_t) * nrows, total_tiles, &a,
+                stream);
+}
+
+}  // extern "C"

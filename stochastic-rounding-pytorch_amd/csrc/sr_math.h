@@ -1,0 +1,291 @@
+// sr_math.h -- element arithmetic of the stochastic-rounding optimizer path.
+//
+// Everything here is a pure function of its arguments, usable on the host
+// (key derivation, CPU-side unit checks) and on gfx950.  Encoders work on the
+// IEEE-754 bit patterns with integer ALU only, so they need no FP mode
+// assumptions.  The FP32 recurrences use explicit fmaf() exactly where the
+// reference's eager CPU kernels fuse, and must be compiled with
+// -ffp-contract=off so that no other multiply-add is contracted.
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define SR_HD __host__ __device__ __forceinline__
+#else
+#include <math.h>
+#define SR_HD static inline
+#endif
+
+namespace sr {
+
+// ---------------------------------------------------------------------------
+// Counter hash and keys (sr_states/_hash.py:5-50).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kHashMul1 = 0x7FEB352Du;
+constexpr uint32_t kHashMul2 = 0x846CA68Bu;
+constexpr uint32_t kKeySalt = 0x9E3779B9u;
+
+// 32-bit avalanche finalizer: two multiplies, three xor-shifts, mod 2^32.
+SR_HD uint32_t h32(uint32_t x) {
+  x ^= x >> 16;
+  x *= kHashMul1;
+  x ^= x >> 15;
+  x *= kHashMul2;
+  return x ^ (x >> 16);
+}
+
+// Update key of one parameter at one optimizer RNG step.  The seed and step
+// enter as their low and high 32-bit words (sr_states/_hash.py:18-23).
+SR_HD uint32_t update_key(uint32_t seed_lo, uint32_t seed_hi, uint32_t step_lo,
+                          uint32_t step_hi, uint32_t param_index) {
+  uint32_t key = h32(seed_lo ^ kKeySalt);
+  key = h32(key ^ seed_hi);
+  key = h32(key ^ step_lo);
+  key = h32(key ^ step_hi);
+  return h32(key ^ param_index);
+}
+
+// Per-state counter base (sr_states/_hash.py:26-28).
+SR_HD uint32_t state_key(uint32_t key, uint32_t state_index) { return h32(key ^ state_index); }
+
+// ---------------------------------------------------------------------------
+// Storage encodings.  `Enc` values index the kernel instantiation tables.
+// ---------------------------------------------------------------------------
+enum Enc : int {
+  ENC_F32 = 0,
+  ENC_BF16_RN = 1,
+  ENC_BF16_SR = 2,
+  ENC_F16_RN = 3,
+  ENC_F16_SR = 4,
+  ENC_E4M3_RN = 5,
+  ENC_E4M3_SR = 6,
+  ENC_E5M2_RN = 7,
+  ENC_E5M2_SR = 8,
+  ENC_COUNT = 9
+};
+
+// Storage width in bytes of an encoding.
+constexpr int enc_bytes(int enc) {
+  return enc == ENC_F32 ? 4 : (enc <= ENC_F16_SR ? 2 : 1);
+}
+constexpr bool enc_stochastic(int enc) {
+  return enc == ENC_BF16_SR || enc == ENC_F16_SR || enc == ENC_E4M3_SR || enc == ENC_E5M2_SR;
+}
+
+SR_HD uint32_t f32_bits(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __float_as_uint(x);
+#else
+  union { float f; uint32_t u; } v;
+  v.f = x;
+  return v.u;
+#endif
+}
+
+SR_HD float bits_f32(uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __uint_as_float(b);
+#else
+  union { float f; uint32_t u; } v;
+  v.u = b;
+  return v.f;
+#endif
+}
+
+// FP32 -> BF16 stochastic rounding (sr_states/_bf16.py:37-74).  For finite
+// input the low 16 bits of the FP32 pattern are the position between the
+// two BF16 neighbours; adding 16 uniform bits and truncating rounds away from
+// zero with exactly that probability.  A carry may reach the next binade or
+// +-Inf.  Inf needs no special case: its low 16 bits are zero, so the sum
+// keeps the Inf pattern.  NaN gets its quiet bit forced so that truncation
+// cannot turn it into Inf.  Written as a select so that it stays branch-free.
+SR_HD uint32_t bf16_sr_bits(uint32_t b, uint32_t hash) {
+  const uint32_t rounded = b + (hash & 0xFFFFu);
+  const uint32_t quieted = b | 0x00400000u;
+  const bool nan = (b & 0x7FFFFFFFu) > 0x7F800000u;
+  return (nan ? quieted : rounded) >> 16;
+}
+
+// FP32 -> BF16 round to nearest, ties to even (torch's Tensor.to(bfloat16)).
+SR_HD uint32_t bf16_rn_bits(uint32_t b) {
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+// Minifloat formats: mantissa bits M, minimum normal exponent EMIN, FP32
+// bits of the largest finite magnitude, saturation policy and storage width
+// (sr_states/_minifloat.py:10-14).
+template <int M, int EMIN, uint32_t MAX_BITS, bool SAT, int WIDTH, uint32_t NAN_ENC, uint32_t INF_ENC>
+struct Minifloat {
+  static constexpr int kM = M;
+  static constexpr int kEmin = EMIN;
+  static constexpr uint32_t kMaxBits = MAX_BITS;
+  static constexpr bool kSat = SAT;
+  static constexpr int kWidth = WIDTH;
+  static constexpr uint32_t kNan = NAN_ENC;
+  static constexpr uint32_t kInf = INF_ENC;  // unused when saturating
+};
+using E4M3 = Minifloat<3, -6, 0x43E00000u /*448*/, true, 8, 0x7Fu, 0u>;
+using E5M2 = Minifloat<2, -14, 0x47600000u /*57344*/, true, 8, 0x7Fu, 0u>;
+using F16 = Minifloat<10, -14, 0x477FE000u /*65504*/, false, 16, 0x7E00u, 0x7C00u>;
+
+// FP32 -> minifloat with nearest-even (STOCH=false) or 24-bit-grid
+// stochastic rounding (STOCH=true), computed on the integer significand.
+//
+// With a = |x| (clamped to the format maximum when saturating) and
+// e = max(exponent(a), EMIN), the target spacing is 2^(e-M).  Writing
+// a / 2^(e-M) = q + r with integer q and 0 <= r < 1:
+//   stochastic: round up iff (hash >> 8) < floor(r * 2^24)
+//   nearest:    round up iff r > 1/2, or r == 1/2 and q is odd
+// (sr_states/_minifloat.py:17-70).  a / 2^(e-M) equals sig * 2^-s for the
+// 24-bit FP32 significand sig and shift s = 150 - M + e - E', so q, r and
+// floor(r * 2^24) are exact integer shifts of sig.  The encoding of the
+// result value (q + up) * 2^(e-M) is ((e - EMIN) << M) + q + up for every
+// finite result: the carry q + up = 2^(M+1) lands on the next binade's
+// encoding, and subnormals (e == EMIN, q < 2^M) need no special case.
+template <class F, bool STOCH>
+SR_HD uint32_t minifloat_bits(uint32_t b, uint32_t hash) {
+  const uint32_t sign = (b >> 31) << (F::kWidth - 1);
+  uint32_t a = b & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return F::kNan | sign;
+  if (F::kSat) {
+    a = a < F::kMaxBits ? a : F::kMaxBits;  // also maps +-Inf to +-max
+  } else if (a == 0x7F800000u) {
+    return F::kInf | sign;
+  }
+  const int E = (int)(a >> 23);
+  const uint32_t sig = E ? ((a & 0x007FFFFFu) | 0x00800000u) : a;
+  const int e_raw = (E ? E : 1) - 127;  // exponent of the significand's unit bit
+  const int e = (E - 127) > F::kEmin ? (E - 127) : F::kEmin;
+  const int s = 23 - F::kM + (e - e_raw);  // >= 23 - M >= 13
+  uint32_t q, up;
+  if (s <= 24) {
+    q = sig >> s;
+    const uint32_t rem = sig & ((1u << s) - 1u);
+    if (STOCH) {
+      up = (hash >> 8) < (rem << (24 - s)) ? 1u : 0u;
+    } else {
+      const uint32_t half = 1u << (s - 1);
+      up = (rem > half || (rem == half && (q & 1u))) ? 1u : 0u;
+    }
+  } else {
+    // a / spacing < 2^(24 - s) <= 1/2: q = 0 and nearest never rounds up.
+    q = 0;
+    const int t = s - 24;
+    up = (STOCH && t < 24 && (hash >> 8) < (sig >> t)) ? 1u : 0u;
+  }
+  uint32_t enc = ((uint32_t)(e - F::kEmin) << F::kM) + q + up;
+  if (!F::kSat) enc = enc < F::kInf ? enc : F::kInf;  // IEEE overflow to Inf
+  return enc | sign;
+}
+
+// Encode an FP32 value into the storage bits of `ENC` with the counter's
+// hash.  The hash is only evaluated for stochastic encodings.
+template <int ENC>
+SR_HD uint32_t encode(float x, uint32_t counter) {
+  const uint32_t b = f32_bits(x);
+  if constexpr (ENC == ENC_F32) {
+    return b;
+  } else if constexpr (ENC == ENC_BF16_RN) {
+    return bf16_rn_bits(b);
+  } else if constexpr (ENC == ENC_BF16_SR) {
+    return bf16_sr_bits(b, h32(counter));
+  } else if constexpr (ENC == ENC_F16_RN) {
+    return minifloat_bits<F16, false>(b, 0);
+  } else if constexpr (ENC == ENC_F16_SR) {
+    return minifloat_bits<F16, true>(b, h32(counter));
+  } else if constexpr (ENC == ENC_E4M3_RN) {
+    return minifloat_bits<E4M3, false>(b, 0);
+  } else if constexpr (ENC == ENC_E4M3_SR) {
+    return minifloat_bits<E4M3, true>(b, h32(counter));
+  } else if constexpr (ENC == ENC_E5M2_RN) {
+    return minifloat_bits<E5M2, false>(b, 0);
+  } else {
+    static_assert(ENC == ENC_E5M2_SR, "unknown encoding");
+    return minifloat_bits<E5M2, true>(b, h32(counter));
+  }
+}
+
+// Exact decode of a minifloat encoding to FP32 (torch's Tensor.float()).
+template <class F>
+SR_HD float minifloat_value(uint32_t v) {
+  constexpr int kExpBits = F::kWidth - 1 - F::kM;
+  constexpr uint32_t kExpMask = (1u << kExpBits) - 1u;
+  const uint32_t sign = (v >> (F::kWidth - 1)) << 31;
+  const uint32_t E = (v >> F::kM) & kExpMask;
+  const uint32_t man = v & ((1u << F::kM) - 1u);
+  if (F::kSat && F::kM == 3) {  // E4M3 (fn): only S.1111.111 is special (NaN)
+    if (E == kExpMask && man == ((1u << F::kM) - 1u)) return bits_f32(sign | 0x7FC00000u);
+  } else if (E == kExpMask) {  // E5M2 / FP16: IEEE Inf and NaN
+    return bits_f32(sign | 0x7F800000u | (man << (23 - F::kM)) | (man ? 0x00400000u : 0u));
+  }
+  if (E == 0) {
+    // man * 2^(EMIN - M): a small integer times a power of two, exact.
+    const float mag = (float)man * bits_f32((uint32_t)(127 + F::kEmin - F::kM) << 23);
+    return bits_f32(f32_bits(mag) | sign);
+  }
+  return bits_f32(sign | ((E - 1u + (uint32_t)(127 + F::kEmin)) << 23) | (man << (23 - F::kM)));
+}
+
+// Decode storage bits of `ENC` to the exact FP32 value.
+template <int ENC>
+SR_HD float decode(uint32_t v) {
+  if constexpr (ENC == ENC_F32) {
+    return bits_f32(v);
+  } else if constexpr (ENC == ENC_BF16_RN || ENC == ENC_BF16_SR) {
+    return bits_f32(v << 16);
+  } else if constexpr (ENC == ENC_F16_RN || ENC == ENC_F16_SR) {
+    return minifloat_value<F16>(v);
+  } else if constexpr (ENC == ENC_E4M3_RN || ENC == ENC_E4M3_SR) {
+    return minifloat_value<E4M3>(v);
+  } else {
+    return minifloat_value<E5M2>(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// FP32 recurrences in the eager reference's operation order.
+// ---------------------------------------------------------------------------
+struct AdamWScalars {
+  float beta1, beta2, one_minus_beta1, one_minus_beta2;
+  float neg_step_size, correction2_sqrt, decay, eps;
+};
+
+// sr_states/reference/adamw.py:86-96:
+//   m' = m*beta1 + (1-beta1)*g          -> fma(g, 1-beta1, m*beta1)
+//   v' = v*beta2 + (1-beta2)*g*g        -> fma((1-beta2)*g, g, v*beta2)
+//   den = sqrt(v') / sqrt(1-beta2^t) + eps
+//   p' = p*(1-lr*wd) + (-lr/(1-beta1^t) * m') / den
+// Every operation is rounded to FP32 on its own; division and square root
+// are IEEE correctly rounded.  The parameter uses the unrounded m'.
+SR_HD void adamw_update(float p, float g, float m, float v, const AdamWScalars& s,
+                        float& p_out, float& m_out, float& v_out) {
+  const float m_scaled = m * s.beta1;
+  m_out = fmaf(g, s.one_minus_beta1, m_scaled);
+  const float g_scaled = s.one_minus_beta2 * g;
+  const float v_scaled = v * s.beta2;
+  v_out = fmaf(g_scaled, g, v_scaled);
+  const float root = sqrtf(v_out);
+  const float den = root / s.correction2_sqrt + s.eps;
+  const float numer = s.neg_step_size * m_out;
+  const float p_decayed = p * s.decay;
+  p_out = p_decayed + numer / den;
+}
+
+struct SgdmScalars {
+  float momentum, neg_lr;
+};
+
+// sr_states/reference/sgd.py:62-64:
+//   u' = u*momentum + g                 (two roundings)
+//   p' = p + (-lr)*u'                   -> fma(u', -lr, p)
+SR_HD void sgdm_update(float p, float g, float u, const SgdmScalars& s, float& p_out,
+                       float& u_out) {
+  const float u_scaled = u * s.momentum;
+  u_out = u_scaled + g;
+  p_out = fmaf(u_out, s.neg_lr, p);
+}
+
+}  // namespace sr

@@ -1,0 +1,44 @@
+"""SR-States for MI355X: stochastic-rounding optimizer states on gfx950.
+
+The public surface follows the reference package ``sr_states``:
+``StateFormat``, ``StateOptimizer``, ``cast`` and ``register_rounding`` at
+the top level, and the fused optimizers and casts in ``sr_states.hip`` (the
+counterpart of ``sr_states.triton``).  All arithmetic runs in the HIP
+library ``libsr_states_hip.so``; there is no CPU execution path.
+"""
+
+from ._hash import state_key, update_key
+from .formats import StateFormat
+from .hip import (
+    AdamWHip,
+    AdamWHipRN,
+    SGDMHip,
+    SGDMHipRN,
+    hip_adamw_step_,
+    hip_sgdm_step_,
+    is_hip_available,
+    rn_cast_bf16,
+    sr_cast_bf16,
+)
+from .optim._state import StateOptimizer
+from .rounding import cast, register_rounding
+
+__all__ = [
+    "AdamWHip",
+    "AdamWHipRN",
+    "SGDMHip",
+    "SGDMHipRN",
+    "StateFormat",
+    "StateOptimizer",
+    "cast",
+    "hip_adamw_step_",
+    "hip_sgdm_step_",
+    "is_hip_available",
+    "register_rounding",
+    "rn_cast_bf16",
+    "sr_cast_bf16",
+    "state_key",
+    "update_key",
+]
+
+__version__ = "0.1.0"

@@ -1,0 +1,156 @@
+"""ctypes binding of libsr_states_hip.so (the C ABI declared in include/sr_states_hip.h).
+
+torch is imported first so that the library's ``libamdhip64.so.7`` dependency
+resolves to the HIP runtime torch already loaded: streams and device pointers
+handed over from torch are then valid in the library.  There is no fallback:
+if the library is missing every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import numpy as np
+import torch  # noqa: F401  (load torch's HIP runtime before the library)
+
+LIBRARY_PATH = Path(__file__).with_name("libsr_states_hip.so")
+ABI_VERSION = 1
+ELEMENTS_PER_THREAD = 8
+MAX_ROWS = 4096
+
+# enum sr_dtype / sr_rule
+SR_F32, SR_BF16, SR_F16, SR_E4M3, SR_E5M2 = range(5)
+SR_NEAREST, SR_STOCHASTIC = 0, 1
+ROW_VECTOR = 1
+ROW_KEYED = 2
+
+DTYPE_CODES = {
+    torch.float32: SR_F32,
+    torch.bfloat16: SR_BF16,
+    torch.float16: SR_F16,
+    torch.float8_e4m3fn: SR_E4M3,
+    torch.float8_e5m2: SR_E5M2,
+}
+RULE_CODES = {"nearest": SR_NEAREST, "stochastic": SR_STOCHASTIC}
+
+# struct sr_row (64 bytes), built on the host and uploaded as bytes.
+ROW_DTYPE = np.dtype(
+    [
+        ("ptr", "<u8", (4,)),
+        ("numel", "<i8"),
+        ("tile_begin", "<u4"),
+        ("tile_end", "<u4"),
+        ("param_index", "<u4"),
+        ("shard_start", "<u4"),
+        ("flags", "<u4"),
+        ("reserved", "<u4"),
+    ]
+)
+assert ROW_DTYPE.itemsize == 64
+
+
+class AdamWHparams(ctypes.Structure):
+    _fields_ = [
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("one_minus_beta1", ctypes.c_float),
+        ("one_minus_beta2", ctypes.c_float),
+        ("neg_step_size", ctypes.c_float),
+        ("correction2_sqrt", ctypes.c_float),
+        ("decay", ctypes.c_float),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class SgdmHparams(ctypes.Structure):
+    _fields_ = [("momentum", ctypes.c_float), ("neg_lr", ctypes.c_float)]
+
+
+_vp, _i64, _u32, _u64, _int = (
+    ctypes.c_void_p,
+    ctypes.c_int64,
+    ctypes.c_uint32,
+    ctypes.c_uint64,
+    ctypes.c_int,
+)
+
+# name -> (restype, argtypes); the complete exported surface of the header.
+SIGNATURES = {
+    "sr_abi_version": (_int, []),
+    "sr_last_error": (ctypes.c_char_p, []),
+    "sr_update_key": (_u32, [_u64, _u64, _u32]),
+    "sr_state_key": (_u32, [_u32, _u32]),
+    "sr_cast": (_int, [_vp, _vp, _i64, _int, _int, _u32, _u32, _int, _vp]),
+    "sr_adamw_step": (
+        _int,
+        [_vp, _vp, _vp, _vp, _i64, _int, _int, _int, _int, _int, _int,
+         ctypes.POINTER(AdamWHparams), _u32, _u32, _int, _vp],
+    ),
+    "sr_adamw_multi": (
+        _int,
+        [_vp, _int, _u32, _int, _int, _int, _int, _int, _int,
+         ctypes.POINTER(AdamWHparams), _u64, _u64, _int, _vp],
+    ),
+    "sr_sgdm_step": (
+        _int,
+        [_vp, _vp, _vp, _i64, _int, _int, _int, _int, ctypes.POINTER(SgdmHparams),
+         _u32, _u32, _int, _vp],
+    ),
+    "sr_sgdm_multi": (
+        _int,
+        [_vp, _int, _u32, _int, _int, _int, _int, ctypes.POINTER(SgdmHparams),
+         _u64, _u64, _int, _vp],
+    ),
+}
+
+_lock = threading.Lock()
+_handle: ctypes.CDLL | None = None
+
+
+def library() -> ctypes.CDLL:
+    """Load the HIP library once; raise if it has not been built."""
+    global _handle
+    if _handle is not None:
+        return _handle
+    with _lock:
+        if _handle is None:
+            if not LIBRARY_PATH.exists():
+                raise RuntimeError(
+                    f"sr_states HIP library not built: {LIBRARY_PATH} is missing "
+                    "(run stochastic-rounding-pytorch_amd/build.py)"
+                )
+            handle = ctypes.CDLL(str(LIBRARY_PATH))
+            for name, (restype, argtypes) in SIGNATURES.items():
+                function = getattr(handle, name)
+                function.restype = restype
+                function.argtypes = argtypes
+            version = handle.sr_abi_version()
+            if version != ABI_VERSION:
+                raise RuntimeError(f"library ABI {version} does not match binding ABI {ABI_VERSION}")
+            _handle = handle
+    return _handle
+
+
+def check(name: str, status: int) -> None:
+    if status != 0:
+        message = library().sr_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({status}): {message}")
+
+
+def call(name: str, *args) -> None:
+    """Call a status-returning entry point and raise RuntimeError on failure."""
+    check(name, getattr(library(), name)(*args))
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def low64(value: int) -> int:
+    return int(value) & 0xFFFFFFFFFFFFFFFF
+
+
+def low32(value: int) -> int:
+    return int(value) & 0xFFFFFFFF

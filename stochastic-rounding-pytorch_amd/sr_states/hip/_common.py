@@ -1,0 +1,36 @@
+"""Device checks for the HIP backend (the gfx950 analogue of triton/_common.py)."""
+
+from __future__ import annotations
+
+from functools import cache
+
+import torch
+
+from .. import _lib
+
+SUPPORTED_ARCH = "gfx950"
+
+
+def is_hip_available() -> bool:
+    """Whether a GPU is visible and the HIP library is built."""
+    return torch.cuda.is_available() and _lib.LIBRARY_PATH.exists()
+
+
+@cache
+def _device_arch(device: torch.device) -> str:
+    return torch.cuda.get_device_properties(device).gcnArchName
+
+
+def validate_device(device: torch.device) -> None:
+    """Reject tensors the gfx950 library cannot run on, before any launch."""
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError("fused state updates require GPU tensors")
+    arch = _device_arch(device).split(":")[0]
+    if arch != SUPPORTED_ARCH:
+        raise ValueError(f"the sr_states HIP library is built for {SUPPORTED_ARCH}, not {arch}")
+
+
+def validate_update_device(device, *dtypes) -> None:
+    """Device check for an optimizer bucket; every storage dtype runs on gfx950."""
+    validate_device(device)

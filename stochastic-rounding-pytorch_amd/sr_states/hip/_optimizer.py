@@ -1,0 +1,65 @@
+"""Validation shared by the fused HIP updates (sr_states/triton/_optimizer.py)."""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from ..rounding import validate_rounding
+
+# Workgroup sizes (threads).  Results do not depend on the choice.
+BLOCK_SIZES = (128, 256, 512, 1024)
+_PARAMETER_DTYPES = (torch.float32, torch.bfloat16)
+
+
+def validate_options(rounding, block_size, state_dtype):
+    validate_rounding(state_dtype, rounding, backend="hip")
+    if block_size not in BLOCK_SIZES:
+        raise ValueError(f"block_size must be one of {BLOCK_SIZES}")
+
+
+def nonnegative(name, value):
+    if not math.isfinite(value) or value < 0:
+        raise ValueError(f"invalid {name}: {value}")
+
+
+def validate_tensor_layout(tensors):
+    """Same device, identical shapes, contiguous; FP32/BF16 parameter and gradient."""
+    parameter, gradient, *_ = tensors
+    device, shape = parameter.device, parameter.shape
+    for tensor in tensors:
+        if tensor.device != device:
+            raise ValueError("all tensors must be on the same GPU device")
+        if tensor.shape != shape:
+            raise ValueError("all tensors must have identical shapes")
+        if not tensor.is_contiguous():
+            raise ValueError("fused state updates require contiguous tensors")
+    if parameter.dtype not in _PARAMETER_DTYPES or gradient.dtype not in _PARAMETER_DTYPES:
+        raise TypeError("parameter and gradient must be FP32 or BF16")
+
+
+def validate_no_overlap(spans):
+    """Sweep (start, end, written) byte spans of one device.
+
+    Gradients are read-only and may share storage with each other; every span
+    the update writes must be disjoint from every other span.
+    """
+    max_end = max_write_end = 0
+    for start, end, write in sorted(spans):
+        if start < (max_end if write else max_write_end):
+            raise ValueError("parameter, gradient, and state must not overlap optimizer writes")
+        max_end = max(max_end, end)
+        if write:
+            max_write_end = max(max_write_end, end)
+
+
+def validate_tensors(parameter, gradient, *states):
+    tensors = (parameter, gradient, *states)
+    if parameter.device.type != "cuda":
+        raise ValueError("fused state updates require GPU tensors")
+    validate_tensor_layout(tensors)
+    if parameter.numel():
+        validate_no_overlap(
+            (t.data_ptr(), t.data_ptr() + t.nbytes, role != 1) for role, t in enumerate(tensors)
+        )

@@ -1,0 +1,215 @@
+"""Fused AdamW on gfx950 with FP32 arithmetic and per-moment storage formats.
+
+Drop-in for sr_states/triton/adamw.py: ``AdamWHip`` takes the arguments of
+``AdamWTriton`` and launches one fused multi-tensor kernel per bucket;
+``hip_adamw_step_`` is the single-tensor functional update.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _lib
+from ..formats import StateFormat, resolve_formats
+from ..optim._state import StateOptimizer
+from ..optim.adamw import adamw_hparams, validate_adamw
+from ..rounding import native_codes
+from ._common import validate_device, validate_update_device
+from ._multi_tensor import prepare_group
+from ._optimizer import nonnegative, validate_options, validate_tensors
+
+
+def _launch(launch, dtypes, hparams, seed, rng_step, block_size, stream):
+    """One sr_adamw_multi call; dtypes = (p, g, m, m_rule, v, v_rule) codes."""
+    _lib.call(
+        "sr_adamw_multi",
+        launch.rows.data_ptr(),
+        launch.nrows,
+        launch.total_tiles,
+        *dtypes,
+        ctypes.byref(hparams),
+        seed,
+        rng_step,
+        block_size,
+        stream,
+    )
+
+
+def _validate_hyperparameters(lr, betas, eps, weight_decay):
+    nonnegative("learning rate", lr)
+    nonnegative("epsilon", eps)
+    nonnegative("weight_decay", weight_decay)
+    if len(betas) != 2 or any(not 0 <= beta < 1 for beta in betas):
+        raise ValueError(f"invalid beta values: {betas}")
+
+
+@torch.no_grad()
+def hip_adamw_step_(
+    parameter: torch.Tensor,
+    gradient: torch.Tensor,
+    exp_avg: torch.Tensor,
+    exp_avg_sq: torch.Tensor,
+    *,
+    lr: float,
+    beta1: float,
+    beta2: float,
+    eps: float,
+    weight_decay: float,
+    step: int,
+    seed: int = 0,
+    offset: int = 0,
+    rounding: str | None = None,
+    formats: tuple | dict | None = None,
+    block_size: int = 256,
+) -> None:
+    """Update parameter and moments in place (triton/adamw.py:160-221).
+
+    Inputs are contiguous, disjoint GPU tensors of one shape; parameter and
+    gradient are FP32 or BF16; each moment uses its own storage format.  The
+    parameter update uses the unrounded FP32 moments.  ``step`` starts at one;
+    ``seed`` is the update key and ``offset`` the flat index of the first
+    element.
+    """
+    if formats is None:
+        rule = "stochastic" if rounding is None else rounding
+        formats = (StateFormat(exp_avg.dtype, rule), StateFormat(exp_avg_sq.dtype, rule))
+        rounding = None
+    resolved = resolve_formats(("exp_avg", "exp_avg_sq"), formats, rounding=rounding, backend="hip")
+    for state, fmt in zip((exp_avg, exp_avg_sq), resolved):
+        validate_options(fmt.rounding, block_size, fmt.dtype)
+        if state.dtype != fmt.dtype:
+            raise ValueError("state dtype does not match its state format")
+    _validate_hyperparameters(lr, (beta1, beta2), eps, weight_decay)
+    if not isinstance(step, int) or isinstance(step, bool) or step < 1:
+        raise ValueError("step must be a positive integer")
+    validate_tensors(parameter, gradient, exp_avg, exp_avg_sq)
+    validate_device(parameter.device)
+    if parameter.numel() == 0:
+        return
+    (m_code, m_rule), (v_code, v_rule) = (native_codes(f.dtype, f.rounding) for f in resolved)
+    hparams = adamw_hparams(lr, beta1, beta2, eps, weight_decay, step)
+    with torch.cuda.device(parameter.device):
+        _lib.call(
+            "sr_adamw_step",
+            parameter.data_ptr(),
+            gradient.data_ptr(),
+            exp_avg.data_ptr(),
+            exp_avg_sq.data_ptr(),
+            parameter.numel(),
+            _lib.DTYPE_CODES[parameter.dtype],
+            _lib.DTYPE_CODES[gradient.dtype],
+            m_code,
+            m_rule,
+            v_code,
+            v_rule,
+            ctypes.byref(hparams),
+            _lib.low32(seed),
+            _lib.low32(offset),
+            block_size,
+            _lib.stream_handle(parameter.device),
+        )
+
+
+class AdamWHip(StateOptimizer):
+    """Fused AdamW with FP32 arithmetic and independently stored moments.
+
+    Same arguments, group keys and checkpoint layout as ``AdamWTriton``
+    (triton/adamw.py:245-319).  ``block_size`` is the workgroup size in
+    threads; results do not depend on it.
+    """
+
+    _state_names = ("exp_avg", "exp_avg_sq")
+    _uses_step = True
+    _rounding_backend = "hip"
+
+    def __init__(
+        self,
+        params,
+        lr=1e-3,
+        betas=(0.9, 0.999),
+        eps=1e-8,
+        weight_decay=1e-2,
+        *,
+        state_format=None,
+        state_dtype=None,
+        rounding=None,
+        seed=0,
+        block_size=256,
+    ):
+        super().__init__(
+            params,
+            {
+                "lr": lr,
+                "betas": betas,
+                "eps": eps,
+                "weight_decay": weight_decay,
+                "block_size": block_size,
+            },
+            state_format=state_format,
+            state_dtype=state_dtype,
+            rounding=rounding,
+            seed=seed,
+        )
+
+    def _group_block_size(self, group):
+        return group.get("block_size", self.defaults["block_size"])
+
+    def _validate_group(self, group):
+        validate_adamw(group)
+        validate_options("nearest", self._group_block_size(group), torch.float32)
+
+    def _step_parameter(self, parameter, state, group, formats, step, seed, offset):
+        beta1, beta2 = group["betas"]
+        hip_adamw_step_(
+            parameter,
+            parameter.grad,
+            state["exp_avg"],
+            state["exp_avg_sq"],
+            lr=group["lr"],
+            beta1=beta1,
+            beta2=beta2,
+            eps=group["eps"],
+            weight_decay=group["weight_decay"],
+            step=step,
+            seed=seed,
+            offset=offset,
+            formats=formats,
+            block_size=self._group_block_size(group),
+        )
+
+    def _step_group(self, group, formats, items, rng_step):
+        items = list(items)
+        if not items:
+            return
+        launches = prepare_group(self, group, formats, items, validate_update_device)
+        beta1, beta2 = group["betas"]
+        (m_code, m_rule), (v_code, v_rule) = (native_codes(f.dtype, f.rounding) for f in formats)
+        seed, rng_word = _lib.low64(group["sr_seed"]), _lib.low64(rng_step)
+        block_size = self._group_block_size(group)
+        for device, step, rows, tables in launches:
+            hparams = adamw_hparams(
+                group["lr"], beta1, beta2, group["eps"], group["weight_decay"], step
+            )
+            parameter, gradient = rows[0].tensors[:2]
+            dtypes = (
+                _lib.DTYPE_CODES[parameter.dtype],
+                _lib.DTYPE_CODES[gradient.dtype],
+                m_code,
+                m_rule,
+                v_code,
+                v_rule,
+            )
+            with torch.cuda.device(device):
+                stream = _lib.stream_handle(device)
+                for launch in tables.launches:
+                    _launch(launch, dtypes, hparams, seed, rng_word, block_size, stream)
+        for _, state, _, step, _ in items:
+            state["step"] = step
+
+
+class AdamWHipRN(AdamWHip):
+    """Fused AdamW whose states always use round-to-nearest storage."""
+
+    _forced_rounding = "nearest"

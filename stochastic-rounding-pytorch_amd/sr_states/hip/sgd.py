@@ -1,0 +1,170 @@
+"""Fused momentum SGD on gfx950 with configurable momentum storage.
+
+Drop-in for sr_states/triton/sgd.py: ``SGDMHip`` takes the arguments of
+``SGDMTriton``; ``hip_sgdm_step_`` is the single-tensor functional update.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _lib
+from ..formats import StateFormat, resolve_formats
+from ..optim._state import StateOptimizer
+from ..optim.sgd import sgdm_hparams, validate_sgdm
+from ..rounding import native_codes
+from ._common import validate_device, validate_update_device
+from ._multi_tensor import prepare_group
+from ._optimizer import nonnegative, validate_options, validate_tensors
+
+
+def _launch(launch, dtypes, hparams, seed, rng_step, block_size, stream):
+    """One sr_sgdm_multi call; dtypes = (p, g, u, u_rule) codes."""
+    _lib.call(
+        "sr_sgdm_multi",
+        launch.rows.data_ptr(),
+        launch.nrows,
+        launch.total_tiles,
+        *dtypes,
+        ctypes.byref(hparams),
+        seed,
+        rng_step,
+        block_size,
+        stream,
+    )
+
+
+@torch.no_grad()
+def hip_sgdm_step_(
+    parameter: torch.Tensor,
+    gradient: torch.Tensor,
+    momentum: torch.Tensor,
+    *,
+    lr: float,
+    momentum_factor: float,
+    seed: int,
+    offset: int = 0,
+    rounding: str | None = None,
+    formats: tuple | dict | None = None,
+    block_size: int = 256,
+) -> None:
+    """Apply one fused momentum-SGD update in place (triton/sgd.py:434-490).
+
+    ``parameter``, ``gradient`` and ``momentum`` are same-shaped contiguous
+    GPU tensors; parameter and gradient are FP32 or BF16 and the momentum uses
+    any built-in storage format.  ``seed`` is the update key and ``offset``
+    the flat index of the first element.
+    """
+    if formats is None:
+        formats = (StateFormat(momentum.dtype, "stochastic" if rounding is None else rounding),)
+        rounding = None
+    resolved = resolve_formats(("momentum_buffer",), formats, rounding=rounding, backend="hip")
+    fmt = resolved[0]
+    validate_options(fmt.rounding, block_size, fmt.dtype)
+    if momentum.dtype != fmt.dtype:
+        raise ValueError("state dtype does not match its state format")
+    nonnegative("learning rate", lr)
+    if not 0 <= momentum_factor < 1:
+        raise ValueError(f"invalid momentum value: {momentum_factor}")
+    validate_tensors(parameter, gradient, momentum)
+    validate_device(parameter.device)
+    if parameter.numel() == 0:
+        return
+    code, rule = native_codes(fmt.dtype, fmt.rounding)
+    hparams = sgdm_hparams(lr, momentum_factor)
+    with torch.cuda.device(parameter.device):
+        _lib.call(
+            "sr_sgdm_step",
+            parameter.data_ptr(),
+            gradient.data_ptr(),
+            momentum.data_ptr(),
+            parameter.numel(),
+            _lib.DTYPE_CODES[parameter.dtype],
+            _lib.DTYPE_CODES[gradient.dtype],
+            code,
+            rule,
+            ctypes.byref(hparams),
+            _lib.low32(seed),
+            _lib.low32(offset),
+            block_size,
+            _lib.stream_handle(parameter.device),
+        )
+
+
+class SGDMHip(StateOptimizer):
+    """Fused momentum SGD; BF16 stochastic momentum storage by default.
+
+    Same arguments, group keys and checkpoint layout as ``SGDMTriton``
+    (triton/sgd.py:493-556).  There is no Nesterov, dampening or weight decay
+    option, as in the reference.
+    """
+
+    _state_names = ("momentum_buffer",)
+    _uses_step = False
+    _rounding_backend = "hip"
+
+    def __init__(
+        self,
+        params,
+        lr,
+        momentum=0.9,
+        *,
+        state_format=None,
+        state_dtype=None,
+        rounding=None,
+        seed=0,
+        block_size=256,
+    ):
+        super().__init__(
+            params,
+            {"lr": lr, "momentum": momentum, "block_size": block_size},
+            state_format=state_format,
+            state_dtype=state_dtype,
+            rounding=rounding,
+            seed=seed,
+        )
+
+    def _group_block_size(self, group):
+        return group.get("block_size", self.defaults["block_size"])
+
+    def _validate_group(self, group):
+        validate_sgdm(group)
+        validate_options("nearest", self._group_block_size(group), torch.float32)
+
+    def _step_parameter(self, parameter, state, group, formats, step, seed, offset):
+        hip_sgdm_step_(
+            parameter,
+            parameter.grad,
+            state["momentum_buffer"],
+            lr=group["lr"],
+            momentum_factor=group["momentum"],
+            seed=seed,
+            offset=offset,
+            formats=formats,
+            block_size=self._group_block_size(group),
+        )
+
+    def _step_group(self, group, formats, items, rng_step):
+        items = list(items)
+        if not items:
+            return
+        launches = prepare_group(self, group, formats, items, validate_update_device)
+        code, rule = native_codes(formats[0].dtype, formats[0].rounding)
+        hparams = sgdm_hparams(group["lr"], group["momentum"])
+        seed, rng_word = _lib.low64(group["sr_seed"]), _lib.low64(rng_step)
+        block_size = self._group_block_size(group)
+        for device, _, rows, tables in launches:
+            parameter, gradient = rows[0].tensors[:2]
+            dtypes = (_lib.DTYPE_CODES[parameter.dtype], _lib.DTYPE_CODES[gradient.dtype], code, rule)
+            with torch.cuda.device(device):
+                stream = _lib.stream_handle(device)
+                for launch in tables.launches:
+                    _launch(launch, dtypes, hparams, seed, rng_word, block_size, stream)
+
+
+class SGDMHipRN(SGDMHip):
+    """Fused momentum SGD whose momentum always uses round-to-nearest storage."""
+
+    _forced_rounding = "nearest"

@@ -1,0 +1,39 @@
+"""AdamW hyperparameters: validation and the FP32 launch scalars."""
+
+from __future__ import annotations
+
+import math
+
+from .. import _lib
+
+
+def validate_adamw(group):
+    """Reject invalid AdamW group values (sr_states/optim/adamw.py:12-18)."""
+    for name in ("lr", "eps", "weight_decay"):
+        if not math.isfinite(group[name]) or group[name] < 0:
+            raise ValueError(f"invalid {name}: {group[name]}")
+    betas = group["betas"]
+    if len(betas) != 2 or any(not 0 <= beta < 1 for beta in betas):
+        raise ValueError(f"invalid beta values: {betas}")
+
+
+def adamw_hparams(lr, beta1, beta2, eps, weight_decay, step) -> _lib.AdamWHparams:
+    """Launch scalars for one bias-correction step.
+
+    The eager reference evaluates each scalar in Python double precision and
+    rounds it to FP32 when it meets an FP32 tensor
+    (sr_states/reference/adamw.py:86-96); ctypes' c_float conversion performs
+    the same round-to-nearest.
+    """
+    bias_correction1 = 1.0 - beta1**step
+    bias_correction2 = 1.0 - beta2**step
+    return _lib.AdamWHparams(
+        beta1=beta1,
+        beta2=beta2,
+        one_minus_beta1=1.0 - beta1,
+        one_minus_beta2=1.0 - beta2,
+        neg_step_size=-lr / bias_correction1,
+        correction2_sqrt=bias_correction2**0.5,
+        decay=1.0 - lr * weight_decay,
+        eps=eps,
+    )

@@ -1,0 +1,20 @@
+"""Momentum-SGD hyperparameters: validation and the FP32 launch scalars."""
+
+from __future__ import annotations
+
+import math
+
+from .. import _lib
+
+
+def validate_sgdm(group):
+    """Reject invalid SGDM group values (sr_states/optim/sgd.py:12-16)."""
+    if not math.isfinite(group["lr"]) or group["lr"] < 0:
+        raise ValueError(f"invalid learning rate: {group['lr']}")
+    if not 0 <= group["momentum"] < 1:
+        raise ValueError(f"invalid momentum value: {group['momentum']}")
+
+
+def sgdm_hparams(lr, momentum) -> _lib.SgdmHparams:
+    """FP32 scalars of ``u = u*momentum + g; p = p + (-lr)*u`` (reference/sgd.py:62-64)."""
+    return _lib.SgdmHparams(momentum=momentum, neg_lr=-lr)

@@ -1,0 +1,121 @@
+"""HIP cast parity: bit-exact against both oracles (NaN payload excluded).
+
+Mirrors the reference's GPU cast tests (tests/test_triton_casts.py,
+tests/test_minifloat_gpu.py:38-50, tests/test_triton_sr_cast.py).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from _cases import boundary_inputs, cast_cases, random_words, rn_midpoint_words
+from conftest import RULES, STATE_DTYPES, assert_bits_or_nan
+
+from oracle import c_oracle, sr_oracle
+
+pytestmark = pytest.mark.gpu
+
+MINIFLOATS = (torch.float16, torch.float8_e4m3fn, torch.float8_e5m2)
+
+
+def _inputs(dtype):
+    parts = [random_words(10007, 541), torch.randn(4099, generator=torch.Generator().manual_seed(5)) * 300]
+    if dtype in MINIFLOATS:
+        parts.append(boundary_inputs(dtype))
+    return torch.cat(parts)
+
+
+@pytest.mark.parametrize("dtype", STATE_DTYPES)
+@pytest.mark.parametrize("rounding", RULES)
+def test_cast_matches_both_oracles(cuda, dtype, rounding):
+    import sr_states
+
+    x = _inputs(dtype)
+    options = {"dtype": dtype, "rounding": rounding, "seed": 2**32 - 7, "offset": 2**32 - 93}
+    expected = sr_oracle.cast(x, **options)
+    assert_bits_or_nan(c_oracle.cast(x, **options), expected, "C oracle vs torch oracle")
+    actual = sr_states.cast(x.to(cuda), **options)
+    assert actual.device == x.to(cuda).device
+    assert_bits_or_nan(actual, expected, f"HIP {dtype} {rounding}")
+
+
+@pytest.mark.parametrize("dtype", STATE_DTYPES)
+@pytest.mark.parametrize("rounding", RULES)
+@pytest.mark.parametrize("block_size,num_warps", [(128, 1), (256, 4), (1024, 8), (4096, 2)])
+def test_cast_launch_shapes_do_not_change_results(cuda, dtype, rounding, block_size, num_warps):
+    from sr_states.hip import cast
+
+    x = _inputs(dtype)
+    options = {"dtype": dtype, "rounding": rounding, "seed": 77, "offset": 2**32 - 19}
+    expected = c_oracle.cast(x, **options)
+    actual = cast(x.to(cuda), block_size=block_size, num_warps=num_warps, **options)
+    assert_bits_or_nan(actual, expected)
+
+
+def test_bf16_cast_contract_cases(cuda):
+    """benchmarks/cast_checks.py:70-80: fresh outputs, input untouched, exact bits."""
+    from sr_states.hip import rn_cast_bf16, sr_cast_bf16
+
+    for x, seed, offset in cast_cases():
+        xd = x.to(cuda)
+        original = xd.view(torch.int32).clone()
+        expected = sr_oracle.stochastic_round_bf16(x, seed=seed, offset=offset)
+        for store_mode in ("convert", "bits"):
+            first = sr_cast_bf16(xd, seed=seed, offset=offset, store_mode=store_mode)
+            second = sr_cast_bf16(xd, seed=seed, offset=offset, store_mode=store_mode)
+            assert_bits_or_nan(first, expected)
+            assert_bits_or_nan(second, expected)
+            if x.numel():
+                assert first.data_ptr() != second.data_ptr()
+                assert first.data_ptr() != xd.data_ptr()
+        assert torch.equal(xd.view(torch.int32), original)
+        assert_bits_or_nan(rn_cast_bf16(xd), x.to(torch.bfloat16))
+    x = rn_midpoint_words()
+    assert_bits_or_nan(rn_cast_bf16(x.to(cuda)), x.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("dtype", STATE_DTYPES)
+def test_stream_partition_invariance(cuda, dtype):
+    import sr_states
+
+    x = torch.linspace(-3, 7, 10003).to(cuda)
+    seed, offset, split = 77, 2**32 - 19, 4101
+    whole = sr_states.cast(x, dtype=dtype, seed=seed, offset=offset)
+    parts = torch.cat(
+        [
+            sr_states.cast(x[:split], dtype=dtype, seed=seed, offset=offset),
+            sr_states.cast(x[split:], dtype=dtype, seed=seed, offset=offset + split),
+        ]
+    )
+    assert_bits_or_nan(parts, whole)
+
+
+def test_unaligned_noncontiguous_and_empty_inputs(cuda):
+    import sr_states
+
+    base = torch.linspace(-1, 1, 4101, device=cuda)
+    unaligned = base[1:]  # 4-byte offset: takes the scalar path
+    expected = c_oracle.cast(unaligned.cpu(), dtype=torch.bfloat16, seed=3, offset=5)
+    assert_bits_or_nan(sr_states.cast(unaligned, dtype=torch.bfloat16, seed=3, offset=5), expected)
+    strided = torch.linspace(-1, 1, 35, device=cuda).reshape(5, 7).T
+    for dtype in STATE_DTYPES:
+        got = sr_states.cast(strided, dtype=dtype, seed=7)
+        assert got.shape == strided.shape
+        assert_bits_or_nan(got, sr_states.cast(strided.contiguous(), dtype=dtype, seed=7))
+        empty = sr_states.cast(torch.empty(0, 3, device=cuda), dtype=dtype)
+        assert empty.shape == (0, 3) and empty.dtype == dtype
+
+
+def test_cast_rejects_invalid_inputs(cuda):
+    from sr_states.hip import cast, rn_cast_bf16, sr_cast_bf16
+
+    with pytest.raises(TypeError, match="float32"):
+        rn_cast_bf16(torch.ones(4, device=cuda, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="contiguous"):
+        rn_cast_bf16(torch.ones(8, device=cuda)[::2])
+    with pytest.raises(ValueError, match="block_size"):
+        sr_cast_bf16(torch.ones(4, device=cuda), seed=1, block_size=3)
+    with pytest.raises(ValueError, match="num_warps"):
+        cast(torch.ones(4, device=cuda), dtype=torch.bfloat16, num_warps=3)
+    with pytest.raises(ValueError, match="store_mode"):
+        sr_cast_bf16(torch.ones(4, device=cuda), seed=1, store_mode="invalid")
