@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SR_ABI_VERSION 1
+#define SR_ABI_VERSION 2
 
 /* Storage dtypes (torch.float32, bfloat16, float16, float8_e4m3fn,
  * float8_e5m2).  The set mirrors the built-in rounding table of the
@@ -54,9 +54,10 @@ enum sr_error {
   SR_ERR_UNSUPPORTED = 3 /* combination not compiled into this library */
 };
 
-/* Elements handled by one thread per tile; a tile is block_size * this many
- * elements.  Hosts use it to lay out the tile ranges of sr_row tables. */
-#define SR_ELEMENTS_PER_THREAD 8
+/* Elements handled by one lane per tile; a tile is block_size * this many
+ * elements and is processed by one workgroup.  Hosts use it to lay out the
+ * tile ranges of sr_row tables. */
+#define SR_ELEMENTS_PER_THREAD 4
 
 /* Row flag: every pointer of the row is 16-byte aligned, so full tiles take
  * the 128-bit vector path.  Rows without it take the coalesced scalar path. */
@@ -66,7 +67,8 @@ enum sr_error {
 #define SR_ROW_KEYED 2u
 
 /* One parameter of a multi-tensor bucket (64 bytes, device memory).
- * Replaces the reference's three tables `meta`, `chunks`, `pointers`
+ * Together with a per-tile row map (uint32 row index per tile) it replaces
+ * the reference's tables `meta`, `chunks` and `pointers`
  * (sr_states/triton/_multi_tensor.py:146-239, consumed by
  * sr_states/triton/_common.py:47-60). */
 typedef struct sr_row {
@@ -138,11 +140,12 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n,
                   uint32_t key, uint32_t offset, int block_size, void* stream);
 
 /* One bucket: `rows` is a device table of nrows sr_row records whose tile
- * ranges cover [0, total_tiles) in order.  Keys are derived on the device
- * from (seed, rng_step, param_index).
+ * ranges cover [0, total_tiles) in order, and `tile_rows` a device array of
+ * total_tiles row indices (tile_rows[t] = the row whose range holds t).
+ * Keys are derived on the device from (seed, rng_step, param_index).
  * Replaces `_multi_adamw_kernel` and its launch
  * (sr_states/triton/adamw.py:102-157, 289-319). */
-int sr_adamw_multi(const sr_row* rows, int nrows, uint32_t total_tiles,
+int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint32_t total_tiles,
                    int p_dtype, int g_dtype, int m_dtype, int m_rule,
                    int v_dtype, int v_rule, const sr_adamw_hparams* hp,
                    uint64_t seed, uint64_t rng_step, int block_size, void* stream);
@@ -155,9 +158,10 @@ int sr_sgdm_step(void* p, const void* g, void* u, int64_t n,
                  const sr_sgdm_hparams* hp, uint32_t key, uint32_t offset,
                  int block_size, void* stream);
 
-/* Replaces `_multi_sgdm_kernel` and its launch
+/* Same table layout as sr_adamw_multi (state 1 pointer unused).
+ * Replaces `_multi_sgdm_kernel` and its launch
  * (sr_states/triton/sgd.py:393-431, 533-556). */
-int sr_sgdm_multi(const sr_row* rows, int nrows, uint32_t total_tiles,
+int sr_sgdm_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint32_t total_tiles,
                   int p_dtype, int g_dtype, int u_dtype, int u_rule,
                   const sr_sgdm_hparams* hp, uint64_t seed, uint64_t rng_step,
                   int block_size, void* stream);

@@ -8,10 +8,7 @@
 
 #include <cstdarg>
 #include <cstdio>
-#include <map>
-#include <mutex>
 #include <string>
-#include <tuple>
 
 #include "../../include/sr_states_hip.h"
 #include "sr_kernels.h"
@@ -77,42 +74,13 @@ int pg_index(int dtype) { return dtype == SR_F32 ? 0 : (dtype == SR_BF16 ? 1 : -
 
 bool valid_block(int block) { return block >= 64 && block <= sr::kMaxBlock && block % 64 == 0; }
 
-// Persistent grid: as many workgroups as fit on the device at once, capped by
-// the number of tiles.  Occupancy is queried once per (device, kernel,
-// block, LDS bytes).
-int grid_size(const void* fn, int block, size_t lds, uint32_t tiles, unsigned* grid) {
-  static std::mutex mu;
-  static std::map<std::tuple<int, const void*, int, size_t>, unsigned> cache;
-  int dev = 0;
-  hipError_t err = hipGetDevice(&dev);
-  if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
-  const auto key = std::make_tuple(dev, fn, block, lds);
-  unsigned resident = 0;
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(key);
-    if (it != cache.end()) resident = it->second;
-  }
-  if (!resident) {
-    int cus = 0, per_cu = 0;
-    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (err != hipSuccess) return hip_fail(err, "hipDeviceGetAttribute");
-    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, lds);
-    if (err != hipSuccess) return hip_fail(err, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
-    if (cus <= 0 || per_cu <= 0) return fail(SR_ERR_HIP, "kernel cannot be resident (block %d)", block);
-    resident = static_cast<unsigned>(cus) * static_cast<unsigned>(per_cu);
-    std::lock_guard<std::mutex> lock(mu);
-    cache[key] = resident;
-  }
-  *grid = tiles < resident ? tiles : resident;
-  return SR_OK;
-}
-
-int launch(const void* fn, int block, size_t lds, uint32_t tiles, void* arg, void* stream) {
-  unsigned grid = 0;
-  if (int rc = grid_size(fn, block, lds, tiles, &grid)) return rc;
+// One workgroup per tile; the grid is padded to a multiple of the XCD count
+// so that the XCD-contiguous tile order of the kernels is a permutation.
+int launch(const void* fn, int block, uint32_t tiles, void* arg, void* stream) {
+  const uint64_t grid = (static_cast<uint64_t>(tiles) + sr::kXcds - 1) / sr::kXcds * sr::kXcds;
+  if (grid > 0x7FFFFFFFull) return fail(SR_ERR_ARGUMENT, "%u tiles exceed the grid limit", tiles);
   void* args[] = {arg};
-  hipError_t err = hipLaunchKernel(fn, dim3(grid), dim3(block), args, lds,
+  hipError_t err = hipLaunchKernel(fn, dim3(static_cast<unsigned>(grid)), dim3(block), args, 0,
                                    static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return hip_fail(err, "hipLaunchKernel");
   return SR_OK;
@@ -120,7 +88,7 @@ int launch(const void* fn, int block, size_t lds, uint32_t tiles, void* arg, voi
 
 // Tiles covering n elements, or fail if they do not fit 32-bit tile indices.
 int tiles_for(int64_t n, int block, uint32_t* tiles) {
-  const int64_t tile = static_cast<int64_t>(block) * sr::kVec;
+  const int64_t tile = static_cast<int64_t>(block) * sr::kEpt;
   const int64_t count = (n + tile - 1) / tile;
   if (count > 0xFFFFFFFFll) return fail(SR_ERR_ARGUMENT, "%lld elements exceed the tile index range", (long long)n);
   *tiles = static_cast<uint32_t>(count);
@@ -164,7 +132,7 @@ int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule, uint32_t see
   a.counter_base = seed + offset;
   a.vector_ok = aligned16(x) && aligned16(y);
   if (int rc = tiles_for(n, block_size, &a.total_tiles)) return rc;
-  return launch(tables().cast[enc], block_size, 0, a.total_tiles, &a, stream);
+  return launch(tables().cast[enc], block_size, a.total_tiles, &a, stream);
 }
 
 int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n, int p_dtype, int g_dtype,
@@ -181,7 +149,7 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n, int p_dty
   if (!p || !g || !m || !v) return fail(SR_ERR_ARGUMENT, "null pointer");
   sr::AdamWArgs a{};
   a.rows = nullptr;
-  a.nrows = 1;
+  a.tile_rows = nullptr;
   a.s = adamw_scalars(*hp);
   if (int rc = tiles_for(n, block_size, &a.total_tiles)) return rc;
   sr_row& r = a.inline_row;
@@ -196,11 +164,11 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n, int p_dty
   r.shard_start = offset;
   r.flags = SR_ROW_KEYED |
             ((aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v)) ? SR_ROW_VECTOR : 0u);
-  return launch(tables().adamw[pi][gi][me][ve], block_size, sizeof(uint32_t), a.total_tiles, &a,
-                stream);
+  return launch(tables().adamw[pi][gi][me][ve], block_size, a.total_tiles, &a, stream);
 }
 
-int sr_adamw_multi(const sr_row* rows, int nrows, uint32_t total_tiles, int p_dtype, int g_dtype,
+int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint32_t total_tiles,
+                   int p_dtype, int g_dtype,
                    int m_dtype, int m_rule, int v_dtype, int v_rule, const sr_adamw_hparams* hp,
                    uint64_t seed, uint64_t rng_step, int block_size, void* stream) {
   const int pi = pg_index(p_dtype), gi = pg_index(g_dtype);
@@ -208,21 +176,19 @@ int sr_adamw_multi(const sr_row* rows, int nrows, uint32_t total_tiles, int p_dt
   if (pi < 0 || gi < 0) return fail(SR_ERR_ARGUMENT, "parameter and gradient must be FP32 or BF16");
   if (me < 0 || ve < 0) return fail(SR_ERR_ARGUMENT, "unsupported state dtype or rule");
   if (!valid_block(block_size)) return fail(SR_ERR_ARGUMENT, "invalid block size %d", block_size);
-  if (!hp || !rows) return fail(SR_ERR_ARGUMENT, "null argument");
-  if (nrows < 1 || nrows > sr::kMaxRows)
-    return fail(SR_ERR_ARGUMENT, "row count %d outside [1, %d]", nrows, sr::kMaxRows);
+  if (!hp || !rows || !tile_rows) return fail(SR_ERR_ARGUMENT, "null argument");
+  if (nrows < 1) return fail(SR_ERR_ARGUMENT, "row count %d below 1", nrows);
   if (total_tiles == 0) return fail(SR_ERR_ARGUMENT, "empty tile range");
   sr::AdamWArgs a{};
   a.rows = rows;
-  a.nrows = static_cast<uint32_t>(nrows);
+  a.tile_rows = tile_rows;
   a.total_tiles = total_tiles;
   a.s = adamw_scalars(*hp);
   a.seed_lo = static_cast<uint32_t>(seed);
   a.seed_hi = static_cast<uint32_t>(seed >> 32);
   a.step_lo = static_cast<uint32_t>(rng_step);
   a.step_hi = static_cast<uint32_t>(rng_step >> 32);
-  return launch(tables().adamw[pi][gi][me][ve], block_size, sizeof(uint32_t) * nrows, total_tiles,
-                &a, stream);
+  return launch(tables().adamw[pi][gi][me][ve], block_size, total_tiles, &a, stream);
 }
 
 int sr_sgdm_step(void* p, const void* g, void* u, int64_t n, int p_dtype, int g_dtype, int u_dtype,
@@ -239,7 +205,7 @@ int sr_sgdm_step(void* p, const void* g, void* u, int64_t n, int p_dtype, int g_
   if (!p || !g || !u) return fail(SR_ERR_ARGUMENT, "null pointer");
   sr::SgdmArgs a{};
   a.rows = nullptr;
-  a.nrows = 1;
+  a.tile_rows = nullptr;
   a.s = {hp->momentum, hp->neg_lr};
   if (int rc = tiles_for(n, block_size, &a.total_tiles)) return rc;
   sr_row& r = a.inline_row;
@@ -253,10 +219,11 @@ int sr_sgdm_step(void* p, const void* g, void* u, int64_t n, int p_dtype, int g_
   r.param_index = key;
   r.shard_start = offset;
   r.flags = SR_ROW_KEYED | ((aligned16(p) && aligned16(g) && aligned16(u)) ? SR_ROW_VECTOR : 0u);
-  return launch(tables().sgdm[pi][gi][ue], block_size, sizeof(uint32_t), a.total_tiles, &a, stream);
+  return launch(tables().sgdm[pi][gi][ue], block_size, a.total_tiles, &a, stream);
 }
 
-int sr_sgdm_multi(const sr_row* rows, int nrows, uint32_t total_tiles, int p_dtype, int g_dtype,
+int sr_sgdm_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint32_t total_tiles,
+                  int p_dtype, int g_dtype,
                   int u_dtype, int u_rule, const sr_sgdm_hparams* hp, uint64_t seed,
                   uint64_t rng_step, int block_size, void* stream) {
   const int pi = pg_index(p_dtype), gi = pg_index(g_dtype);
@@ -264,21 +231,19 @@ int sr_sgdm_multi(const sr_row* rows, int nrows, uint32_t total_tiles, int p_dty
   if (pi < 0 || gi < 0) return fail(SR_ERR_ARGUMENT, "parameter and gradient must be FP32 or BF16");
   if (ue < 0) return fail(SR_ERR_ARGUMENT, "unsupported state dtype or rule");
   if (!valid_block(block_size)) return fail(SR_ERR_ARGUMENT, "invalid block size %d", block_size);
-  if (!hp || !rows) return fail(SR_ERR_ARGUMENT, "null argument");
-  if (nrows < 1 || nrows > sr::kMaxRows)
-    return fail(SR_ERR_ARGUMENT, "row count %d outside [1, %d]", nrows, sr::kMaxRows);
+  if (!hp || !rows || !tile_rows) return fail(SR_ERR_ARGUMENT, "null argument");
+  if (nrows < 1) return fail(SR_ERR_ARGUMENT, "row count %d below 1", nrows);
   if (total_tiles == 0) return fail(SR_ERR_ARGUMENT, "empty tile range");
   sr::SgdmArgs a{};
   a.rows = rows;
-  a.nrows = static_cast<uint32_t>(nrows);
+  a.tile_rows = tile_rows;
   a.total_tiles = total_tiles;
   a.s = {hp->momentum, hp->neg_lr};
   a.seed_lo = static_cast<uint32_t>(seed);
   a.seed_hi = static_cast<uint32_t>(seed >> 32);
   a.step_lo = static_cast<uint32_t>(rng_step);
   a.step_hi = static_cast<uint32_t>(rng_step >> 32);
-  return launch(tables().sgdm[pi][gi][ue], block_size, sizeof(uint32_t) * nrows, total_tiles, &a,
-                stream);
+  return launch(tables().sgdm[pi][gi][ue], block_size, total_tiles, &a, stream);
 }
 
 }  // extern "C"

@@ -16,9 +16,8 @@ import numpy as np
 import torch  # noqa: F401  (load torch's HIP runtime before the library)
 
 LIBRARY_PATH = Path(__file__).with_name("libsr_states_hip.so")
-ABI_VERSION = 1
-ELEMENTS_PER_THREAD = 8
-MAX_ROWS = 4096
+ABI_VERSION = 2
+ELEMENTS_PER_THREAD = 4
 
 # enum sr_dtype / sr_rule
 SR_F32, SR_BF16, SR_F16, SR_E4M3, SR_E5M2 = range(5)
@@ -90,7 +89,7 @@ SIGNATURES = {
     ),
     "sr_adamw_multi": (
         _int,
-        [_vp, _int, _u32, _int, _int, _int, _int, _int, _int,
+        [_vp, _vp, _int, _u32, _int, _int, _int, _int, _int, _int,
          ctypes.POINTER(AdamWHparams), _u64, _u64, _int, _vp],
     ),
     "sr_sgdm_step": (
@@ -100,7 +99,7 @@ SIGNATURES = {
     ),
     "sr_sgdm_multi": (
         _int,
-        [_vp, _int, _u32, _int, _int, _int, _int, ctypes.POINTER(SgdmHparams),
+        [_vp, _vp, _int, _u32, _int, _int, _int, _int, ctypes.POINTER(SgdmHparams),
          _u64, _u64, _int, _vp],
     ),
 }

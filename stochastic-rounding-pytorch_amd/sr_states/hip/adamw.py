@@ -21,13 +21,14 @@ from ._multi_tensor import prepare_group
 from ._optimizer import nonnegative, validate_options, validate_tensors
 
 
-def _launch(launch, dtypes, hparams, seed, rng_step, block_size, stream):
+def _launch(tables, dtypes, hparams, seed, rng_step, block_size, stream):
     """One sr_adamw_multi call; dtypes = (p, g, m, m_rule, v, v_rule) codes."""
     _lib.call(
         "sr_adamw_multi",
-        launch.rows.data_ptr(),
-        launch.nrows,
-        launch.total_tiles,
+        tables.device_records.data_ptr(),
+        tables.device_tile_rows.data_ptr(),
+        tables.nrows,
+        tables.total_tiles,
         *dtypes,
         ctypes.byref(hparams),
         seed,
@@ -202,9 +203,9 @@ class AdamWHip(StateOptimizer):
                 v_rule,
             )
             with torch.cuda.device(device):
-                stream = _lib.stream_handle(device)
-                for launch in tables.launches:
-                    _launch(launch, dtypes, hparams, seed, rng_word, block_size, stream)
+                _launch(
+                    tables, dtypes, hparams, seed, rng_word, block_size, _lib.stream_handle(device)
+                )
         for _, state, _, step, _ in items:
             state["step"] = step
 

@@ -20,13 +20,14 @@ from ._multi_tensor import prepare_group
 from ._optimizer import nonnegative, validate_options, validate_tensors
 
 
-def _launch(launch, dtypes, hparams, seed, rng_step, block_size, stream):
+def _launch(tables, dtypes, hparams, seed, rng_step, block_size, stream):
     """One sr_sgdm_multi call; dtypes = (p, g, u, u_rule) codes."""
     _lib.call(
         "sr_sgdm_multi",
-        launch.rows.data_ptr(),
-        launch.nrows,
-        launch.total_tiles,
+        tables.device_records.data_ptr(),
+        tables.device_tile_rows.data_ptr(),
+        tables.nrows,
+        tables.total_tiles,
         *dtypes,
         ctypes.byref(hparams),
         seed,
@@ -159,9 +160,9 @@ class SGDMHip(StateOptimizer):
             parameter, gradient = rows[0].tensors[:2]
             dtypes = (_lib.DTYPE_CODES[parameter.dtype], _lib.DTYPE_CODES[gradient.dtype], code, rule)
             with torch.cuda.device(device):
-                stream = _lib.stream_handle(device)
-                for launch in tables.launches:
-                    _launch(launch, dtypes, hparams, seed, rng_word, block_size, stream)
+                _launch(
+                    tables, dtypes, hparams, seed, rng_word, block_size, _lib.stream_handle(device)
+                )
 
 
 class SGDMHipRN(SGDMHip):
