@@ -74,6 +74,18 @@ WORKLOADS = {
         hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
         seed=7,
     ),
+    # A plain device copy of known size (4 GiB read + 4 GiB written per step);
+    # its rocprofv3 FETCH_SIZE / WRITE_SIZE readings calibrate the counters.
+    "copy_calibration": dict(
+        optimizer="copy",
+        shapes=[(1 << 30,)],
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=(),
+        grad_std=1.0,
+        hparams={},
+        seed=0,
+    ),
     "c5_sgdm_fp16": dict(
         optimizer="sgdm",
         shapes=[(2048, 2048)] * 256,
@@ -89,6 +101,8 @@ WORKLOADS = {
 
 def bytes_per_element(spec) -> int:
     size = lambda dt: torch.empty((), dtype=dt).element_size()  # noqa: E731
+    if spec["optimizer"] == "copy":
+        return 2 * size(spec["p_dtype"])
     states = sum(2 * size(dt) for dt, _ in spec["formats"])
     return 2 * size(spec["p_dtype"]) + size(spec["g_dtype"]) + states
 
@@ -106,10 +120,15 @@ class _Param(torch.nn.Parameter):
 
 
 def build(spec, device):
+    """(tensors, step callable) of a workload, inputs resident on `device`."""
     import sr_states
     from sr_states import StateFormat
 
     gen = torch.Generator(device=device).manual_seed(spec["seed"])
+    if spec["optimizer"] == "copy":
+        src = torch.empty(spec["shapes"][0], device=device).normal_(generator=gen)
+        dst = torch.empty_like(src)
+        return [src], lambda: dst.copy_(src)
     params = []
     for shape in spec["shapes"]:
         p = _Param(torch.empty(shape, device=device, dtype=spec["p_dtype"]))
@@ -124,7 +143,7 @@ def build(spec, device):
         opt = sr_states.AdamWHip(params, state_format=formats, seed=spec["seed"], **spec["hparams"])
     else:
         opt = sr_states.SGDMHip(params, state_format=formats, seed=spec["seed"], **spec["hparams"])
-    return params, opt
+    return params, opt.step
 
 
 def cpu_baseline(spec, target_seconds: float = 12.0):
@@ -160,12 +179,13 @@ def cpu_baseline(spec, target_seconds: float = 12.0):
     }
 
 
-def load_traffic(workload: str, bytes_per_launch: float):
-    path = ROOT / "profiles" / f"traffic_{workload}.json"
-    if not path.exists():
-        return None
-    data = json.loads(path.read_text())
-    return data.get("hbm_bytes_per_launch")
+def load_traffic(workload: str):
+    """HBM bytes per launch from the committed rocprofv3 FETCH/WRITE summary, or None."""
+    for path in sorted((ROOT / "profiles").glob(f"*_{workload}_hbm_traffic.md")):
+        for line in path.read_text().splitlines():
+            if line.startswith("hbm_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    return None
 
 
 def main():
@@ -186,10 +206,10 @@ def main():
         raise SystemExit("bench.py needs a GPU")
     spec = WORKLOADS[args.workload]
     device = torch.device("cuda", 0)
-    params, opt = build(spec, device)
+    params, step = build(spec, device)
     elements = sum(p.numel() for p in params)
     for _ in range(args.warmup):
-        opt.step()
+        step()
     torch.cuda.synchronize()
 
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
@@ -200,7 +220,7 @@ def main():
     total_start.record()
     for i in range(args.steps):
         starts[i].record()
-        opt.step()
+        step()
         ends[i].record()
     total_end.record()
     torch.cuda.synchronize()
@@ -211,11 +231,14 @@ def main():
     bpe = bytes_per_element(spec)
     bytes_per_launch = bpe * elements
     achieved = bytes_per_launch / (kernel_ms / 1e3) / 1e9
-    traffic = load_traffic(args.workload, bytes_per_launch)
+    traffic = load_traffic(args.workload)
     dtype = "f32"
     result = {
-        "metric": "AdamW-SR step: params updated/sec and achieved HBM GB/s (% of peak), 1 MI355X"
-        if spec["optimizer"] == "adamw" else "SGDM-SR step: params updated/sec, 1 MI355X",
+        "metric": {
+            "adamw": "AdamW-SR step: params updated/sec and achieved HBM GB/s (% of peak), 1 MI355X",
+            "sgdm": "SGDM-SR step: params updated/sec and achieved HBM GB/s (% of peak), 1 MI355X",
+            "copy": "device copy (counter calibration): elements/sec, 1 MI355X",
+        }[spec["optimizer"]],
         "value": elements / (ms_per_step / 1e3),
         "unit": "params/s",
         "n_gpus": 1,
@@ -250,8 +273,8 @@ def main():
         },
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline:
-        del params, opt
+    if not args.no_cpu_baseline and spec["optimizer"] != "copy":
+        del params, step
         torch.cuda.empty_cache()
         result["cpu_baseline"] = cpu_baseline(spec, args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -31,7 +31,7 @@
 namespace sr {
 
 constexpr int kEpt = SR_ELEMENTS_PER_THREAD;
-static_assert(kEpt == 4, "the vector paths below move 4 elements per lane");
+static_assert(kEpt == 2 || kEpt == 4 || kEpt == 8, "lanes move 2, 4 or 8 elements");
 constexpr int kMaxBlock = 1024;
 constexpr uint32_t kXcds = 8;
 
@@ -88,36 +88,61 @@ __device__ __forceinline__ SR_GLOBAL T* gptr_mut(void* p) {
   return (SR_GLOBAL T*)(p);
 }
 
-// 4 elements at index i (i a multiple of 4, base 16-byte aligned).
-template <int ENC>
-__device__ __forceinline__ void load4(const void* base, int64_t i, uint32_t (&raw)[kEpt]) {
-  constexpr int W = enc_bytes(ENC);
-  const char* ptr = static_cast<const char*>(base) + i * W;
-  if constexpr (W == 4) {
+// kEpt elements at index i (i a multiple of kEpt, base 16-byte aligned),
+// moved as one access of kEpt * width bytes (two for 32 bytes).
+template <int BYTES>
+__device__ __forceinline__ void load_words(const char* ptr, uint32_t* w) {
+  if constexpr (BYTES == 32) {
+    const uint4 a = *gptr<uint4>(ptr), b = *gptr<uint4>(ptr + 16);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  } else if constexpr (BYTES == 16) {
     const uint4 a = *gptr<uint4>(ptr);
-    raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
-  } else if constexpr (W == 2) {
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  } else if constexpr (BYTES == 8) {
     const uint2 a = *gptr<uint2>(ptr);
-    raw[0] = a.x & 0xFFFFu; raw[1] = a.x >> 16;
-    raw[2] = a.y & 0xFFFFu; raw[3] = a.y >> 16;
+    w[0] = a.x; w[1] = a.y;
+  } else if constexpr (BYTES == 4) {
+    w[0] = *gptr<uint32_t>(ptr);
   } else {
-    const uint32_t a = *gptr<uint32_t>(ptr);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) raw[k] = (a >> (8 * k)) & 0xFFu;
+    static_assert(BYTES == 2, "unsupported access width");
+    w[0] = *gptr<uint16_t>(ptr);
+  }
+}
+
+template <int BYTES>
+__device__ __forceinline__ void store_words(char* ptr, const uint32_t* w) {
+  if constexpr (BYTES == 32) {
+    *gptr_mut<uint4>(ptr) = make_uint4(w[0], w[1], w[2], w[3]);
+    *gptr_mut<uint4>(ptr + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+  } else if constexpr (BYTES == 16) {
+    *gptr_mut<uint4>(ptr) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else if constexpr (BYTES == 8) {
+    *gptr_mut<uint2>(ptr) = make_uint2(w[0], w[1]);
+  } else if constexpr (BYTES == 4) {
+    *gptr_mut<uint32_t>(ptr) = w[0];
+  } else {
+    static_assert(BYTES == 2, "unsupported access width");
+    *gptr_mut<uint16_t>(ptr) = static_cast<uint16_t>(w[0]);
   }
 }
 
 template <int ENC>
-__device__ __forceinline__ void store4(void* base, int64_t i, const uint32_t (&raw)[kEpt]) {
-  constexpr int W = enc_bytes(ENC);
-  char* ptr = static_cast<char*>(base) + i * W;
-  if constexpr (W == 4) {
-    *gptr_mut<uint4>(ptr) = make_uint4(raw[0], raw[1], raw[2], raw[3]);
-  } else if constexpr (W == 2) {
-    *gptr_mut<uint2>(ptr) = make_uint2(raw[0] | (raw[1] << 16), raw[2] | (raw[3] << 16));
-  } else {
-    *gptr_mut<uint32_t>(ptr) = raw[0] | (raw[1] << 8) | (raw[2] << 16) | (raw[3] << 24);
-  }
+__device__ __forceinline__ void load_vec(const void* base, int64_t i, uint32_t (&raw)[kEpt]) {
+  constexpr int W = enc_bytes(ENC), BYTES = kEpt * W;
+  constexpr uint32_t mask = W == 4 ? 0xFFFFFFFFu : (1u << (8 * W)) - 1u;
+  uint32_t w[(BYTES + 3) / 4];
+  load_words<BYTES>(static_cast<const char*>(base) + i * W, w);
+#pragma unroll
+  for (int k = 0; k < kEpt; ++k) raw[k] = (w[k * W / 4] >> (8 * ((k * W) % 4))) & mask;
+}
+
+template <int ENC>
+__device__ __forceinline__ void store_vec(void* base, int64_t i, const uint32_t (&raw)[kEpt]) {
+  constexpr int W = enc_bytes(ENC), BYTES = kEpt * W;
+  uint32_t w[(BYTES + 3) / 4] = {};
+#pragma unroll
+  for (int k = 0; k < kEpt; ++k) w[k * W / 4] |= raw[k] << (8 * ((k * W) % 4));
+  store_words<BYTES>(static_cast<char*>(base) + i * W, w);
 }
 
 template <int ENC>
@@ -156,10 +181,10 @@ template <int PE, int GE, int ME, int VE>
 __device__ __forceinline__ void adamw_vector(char* p, const char* g, char* m, char* v, int64_t i,
                                              uint32_t cm, uint32_t cv, const AdamWScalars& s) {
   uint32_t rp[kEpt], rg[kEpt], rm[kEpt], rv[kEpt];
-  load4<PE>(p, i, rp);
-  load4<GE>(g, i, rg);
-  load4<ME>(m, i, rm);
-  load4<VE>(v, i, rv);
+  load_vec<PE>(p, i, rp);
+  load_vec<GE>(g, i, rg);
+  load_vec<ME>(m, i, rm);
+  load_vec<VE>(v, i, rv);
   const uint32_t base = static_cast<uint32_t>(i);
 #pragma unroll
   for (int k = 0; k < kEpt; ++k) {
@@ -170,9 +195,9 @@ __device__ __forceinline__ void adamw_vector(char* p, const char* g, char* m, ch
     rm[k] = encode<ME>(mo, cm + base + k);
     rv[k] = encode<VE>(vo, cv + base + k);
   }
-  store4<PE>(p, i, rp);
-  store4<ME>(m, i, rm);
-  store4<VE>(v, i, rv);
+  store_vec<PE>(p, i, rp);
+  store_vec<ME>(m, i, rm);
+  store_vec<VE>(v, i, rv);
 }
 
 template <int PE, int GE, int ME, int VE>
@@ -221,9 +246,9 @@ template <int PE, int GE, int UE>
 __device__ __forceinline__ void sgdm_vector(char* p, const char* g, char* u, int64_t i, uint32_t cu,
                                             const SgdmScalars& s) {
   uint32_t rp[kEpt], rg[kEpt], ru[kEpt];
-  load4<PE>(p, i, rp);
-  load4<GE>(g, i, rg);
-  load4<UE>(u, i, ru);
+  load_vec<PE>(p, i, rp);
+  load_vec<GE>(g, i, rg);
+  load_vec<UE>(u, i, ru);
   const uint32_t base = static_cast<uint32_t>(i);
 #pragma unroll
   for (int k = 0; k < kEpt; ++k) {
@@ -232,8 +257,8 @@ __device__ __forceinline__ void sgdm_vector(char* p, const char* g, char* u, int
     rp[k] = encode<PE>(po, 0);
     ru[k] = encode<UE>(uo, cu + base + k);
   }
-  store4<PE>(p, i, rp);
-  store4<UE>(u, i, ru);
+  store_vec<PE>(p, i, rp);
+  store_vec<UE>(u, i, ru);
 }
 
 template <int PE, int GE, int UE>
@@ -281,11 +306,11 @@ __global__ __launch_bounds__(kMaxBlock) void cast_kernel(const CastArgs a) {
   if (a.vector_ok && start + tile <= a.n) {
     const int64_t i = start + static_cast<int64_t>(threadIdx.x) * kEpt;
     uint32_t r[kEpt];
-    load4<ENC_F32>(a.x, i, r);
+    load_vec<ENC_F32>(a.x, i, r);
     const uint32_t base = a.counter_base + static_cast<uint32_t>(i);
 #pragma unroll
     for (int k = 0; k < kEpt; ++k) r[k] = encode<ENC>(bits_f32(r[k]), base + k);
-    store4<ENC>(a.y, i, r);
+    store_vec<ENC>(a.y, i, r);
   } else {
 #pragma unroll
     for (int k = 0; k < kEpt; ++k) {

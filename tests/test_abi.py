@@ -1,0 +1,86 @@
+"""The C ABI library loads, exports every declared symbol, and validates arguments (CPU).
+
+No call here reaches the GPU: the argument checks of each entry point run
+before any HIP call, so invalid arguments return an error code on a machine
+without a GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "sr_states_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(sr_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_expected_surface():
+    assert declared_functions() == sorted(
+        [
+            "sr_abi_version",
+            "sr_last_error",
+            "sr_update_key",
+            "sr_state_key",
+            "sr_cast",
+            "sr_adamw_step",
+            "sr_adamw_multi",
+            "sr_sgdm_step",
+            "sr_sgdm_multi",
+        ]
+    )
+
+
+def test_library_exports_every_declared_symbol():
+    from sr_states import _lib
+
+    handle = _lib.library()
+    for name in declared_functions():
+        assert hasattr(handle, name), name
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+    assert handle.sr_abi_version() == _lib.ABI_VERSION
+
+
+def test_header_constants_match_the_binding():
+    from sr_states import _lib
+
+    text = HEADER.read_text()
+    assert f"#define SR_ABI_VERSION {_lib.ABI_VERSION}" in text
+    assert f"#define SR_ELEMENTS_PER_THREAD {_lib.ELEMENTS_PER_THREAD}" in text
+    assert "#define SR_ROW_VECTOR 1u" in text and _lib.ROW_VECTOR == 1
+    assert "#define SR_ROW_KEYED 2u" in text and _lib.ROW_KEYED == 2
+    assert _lib.ROW_DTYPE.itemsize == 64
+    assert ctypes.sizeof(_lib.AdamWHparams) == 32 and ctypes.sizeof(_lib.SgdmHparams) == 8
+
+
+def test_invalid_arguments_fail_before_any_device_work():
+    from sr_states import _lib
+
+    lib = _lib.library()
+    assert lib.sr_cast(None, None, 16, 9, 0, 0, 0, 256, None) == 1
+    assert b"unsupported cast dtype" in lib.sr_last_error()
+    assert lib.sr_cast(None, None, 16, 1, 1, 0, 0, 100, None) == 1
+    assert b"block size" in lib.sr_last_error()
+    assert lib.sr_cast(None, None, 0, 1, 1, 0, 0, 256, None) == 0  # empty: nothing to do
+    hp = _lib.AdamWHparams()
+    assert lib.sr_adamw_step(None, None, None, None, 8, 2, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, 256, None) == 1
+    assert b"FP32 or BF16" in lib.sr_last_error()
+    assert lib.sr_adamw_multi(None, None, 1, 1, 0, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, 256, None) == 1
+    assert b"null argument" in lib.sr_last_error()
+    sp = _lib.SgdmHparams()
+    assert lib.sr_sgdm_multi(None, None, 0, 1, 0, 0, 7, 1, ctypes.byref(sp), 0, 0, 256, None) == 1
+    assert b"unsupported state" in lib.sr_last_error()
+
+
+def test_call_raises_with_the_library_message():
+    from sr_states import _lib
+
+    with pytest.raises(RuntimeError, match="unsupported cast dtype"):
+        _lib.call("sr_cast", None, None, 16, 9, 0, 0, 0, 256, None)

@@ -1,0 +1,315 @@
+"""Host-side API contract (CPU): formats, rounding registry, validation, checkpoints.
+
+Mirrors tests/test_state_formats.py, tests/test_rounding_registry.py,
+tests/test_state_optimizers.py:13-45,110-127, tests/test_triton_api.py and
+tests/test_rng_streams.py:180-215 of the reference.  Nothing here launches a
+kernel.
+"""
+
+from __future__ import annotations
+
+import copy
+import io
+from pathlib import Path
+
+import pytest
+import torch
+
+import sr_states
+import sr_states.rounding as rounding_module
+from sr_states import AdamWHip, AdamWHipRN, SGDMHip, SGDMHipRN, StateFormat, cast, register_rounding
+from sr_states.rounding import validate_rounding
+
+CLASSES = [AdamWHip, SGDMHip]
+GOLDEN = Path(__file__).parent / "golden" / "reference_trajectories.pt"
+
+
+@pytest.fixture(autouse=True)
+def isolated_registry(monkeypatch):
+    monkeypatch.setattr(rounding_module, "_ROUTINES", rounding_module._ROUTINES.copy())
+
+
+def bits(x):
+    return x.contiguous().view(torch.uint8)
+
+
+def toward_zero(x, *, dtype, seed, offset):
+    return (x.contiguous().view(torch.int32) & -65536).view(torch.float32).to(dtype)
+
+
+# -- formats ------------------------------------------------------------------
+def test_state_format_serialization_and_backends():
+    fmt = StateFormat(torch.bfloat16, "nearest")
+    assert StateFormat.from_dict(fmt.to_dict()) == fmt
+    fmt.validate("reference")
+    fmt.validate("hip")
+    with pytest.raises(ValueError, match="backend"):
+        fmt.validate("missing")
+    for invalid in ({"dtype": torch.bfloat16}, {"dtype": torch.bfloat16, "rounding": "nearest", "extra": 1}):
+        with pytest.raises(ValueError):
+            StateFormat.from_dict(invalid)
+    assert StateFormat(torch.float8_e4m3fn).to_dict() == {"dtype": torch.float8_e4m3fn, "rounding": "stochastic"}
+
+
+@pytest.mark.parametrize("cls", CLASSES)
+def test_format_validation_and_group_overrides(cls):
+    """tests/test_state_formats.py:103-134."""
+    p, q = [torch.nn.Parameter(torch.ones(3)) for _ in range(2)]
+    fmt = StateFormat(torch.float32, "nearest")
+    for extra in ({"state_dtype": torch.float32}, {"rounding": "nearest"}):
+        with pytest.raises(ValueError, match="combined"):
+            cls([p], lr=0.1, state_format=fmt, **extra)
+    with pytest.raises(TypeError, match="StateFormat"):
+        cls([{"params": [p], "state_format": (fmt,) * len(cls._state_names)}], lr=0.1)
+    with pytest.raises(ValueError, match="keys"):
+        cls([p], lr=0.1, state_format={"bad": fmt})
+    opt = cls([{"params": [p], "state_format": fmt}], lr=0.1)
+    assert all(f["dtype"] == torch.float32 for f in opt.param_groups[0]["state_format"].values())
+    opt.add_param_group({"params": [q], "rounding": "nearest"})
+    assert all(f == StateFormat(torch.bfloat16, "nearest").to_dict()
+               for f in opt.param_groups[1]["state_format"].values())
+    with pytest.raises(ValueError, match="registered"):
+        opt.add_param_group({"params": [torch.nn.Parameter(torch.ones(1))],
+                             "state_format": StateFormat(torch.bfloat16, "missing")})
+    assert len(opt.param_groups) == 2
+    with pytest.raises(ValueError):
+        opt.add_param_group({"params": [torch.nn.Parameter(torch.ones(1))], "lr": -1})
+    assert len(opt.param_groups) == 2
+
+
+def test_shorthand_single_and_dict_formats_serialize_identically():
+    fmt = StateFormat(torch.float8_e5m2, "nearest")
+    p = torch.nn.Parameter(torch.ones(2))
+    variants = [{"state_dtype": fmt.dtype, "rounding": fmt.rounding}, {"state_format": fmt},
+                {"state_format": dict.fromkeys(AdamWHip._state_names, fmt)}]
+    groups = [AdamWHip([p], **v).param_groups[0]["state_format"] for v in variants]
+    assert groups[0] == groups[1] == groups[2]
+
+
+@pytest.mark.parametrize("rn,sr", [(AdamWHipRN, AdamWHip), (SGDMHipRN, SGDMHip)])
+def test_rn_classes_force_nearest(rn, sr):
+    """tests/test_state_formats.py:258-293 (host part)."""
+    dtypes = (torch.float8_e4m3fn, torch.float8_e5m2)
+    per_state = {n: StateFormat(d) for n, d in zip(rn._state_names, dtypes)}
+    nearest = {n: StateFormat(d, "nearest") for n, d in zip(rn._state_names, dtypes)}
+    opt = rn([torch.nn.Parameter(torch.ones(3))], lr=0.01, state_format=per_state, seed=5)
+    expected = sr([torch.nn.Parameter(torch.ones(3))], lr=0.01, state_format=nearest, seed=5)
+    assert opt.param_groups[0]["state_format"] == expected.param_groups[0]["state_format"]
+    for override in ({"state_format": StateFormat(torch.bfloat16)}, {"rounding": "stochastic"}):
+        opt.add_param_group({"params": [torch.nn.Parameter(torch.ones(2))], **override})
+        assert all(f["rounding"] == "nearest" for f in opt.param_groups[-1]["state_format"].values())
+    with pytest.raises(ValueError, match="combined"):
+        rn([torch.nn.Parameter(torch.ones(1))], lr=0.01, state_format=per_state, rounding="nearest")
+
+
+# -- registry ------------------------------------------------------------------
+def test_registration_validation_and_builtins():
+    """tests/test_rounding_registry.py:113-128."""
+    with pytest.raises(ValueError, match="already registered"):
+        register_rounding("nearest", torch.bfloat16, reference=toward_zero)
+    with pytest.raises(ValueError, match="nonempty"):
+        register_rounding("", torch.bfloat16, reference=toward_zero)
+    with pytest.raises(ValueError, match="floating-point"):
+        register_rounding("rule", torch.int32, reference=toward_zero)
+    with pytest.raises(TypeError, match="callable"):
+        register_rounding("rule", torch.bfloat16, reference=None)
+    for dtype in (torch.float32, torch.bfloat16, torch.float16, torch.float8_e4m3fn, torch.float8_e5m2):
+        for mode in ("nearest", "stochastic"):
+            validate_rounding(dtype, mode, backend="hip")
+            with pytest.raises(ValueError, match="already registered"):
+                register_rounding(mode, dtype, reference=toward_zero)
+    with pytest.raises(ValueError, match="backend"):
+        validate_rounding(torch.bfloat16, "nearest", backend="unknown")
+
+
+def test_custom_rule_cast_contract():
+    """tests/test_rounding_registry.py:131-139: custom routines run as registered."""
+    register_rounding("toward_zero", torch.bfloat16, reference=toward_zero)
+    x = torch.tensor([1.003, -1.006, 0.0])
+    assert torch.equal(cast(x, dtype=torch.bfloat16, rounding="toward_zero"), toward_zero(x, dtype=torch.bfloat16, seed=0, offset=0))
+    register_rounding("bad_dtype", torch.bfloat16, reference=lambda x, **kw: x)
+    register_rounding("bad_shape", torch.bfloat16, reference=lambda x, **kw: x[:1].bfloat16())
+    register_rounding("not_tensor", torch.bfloat16, reference=lambda x, **kw: None)
+    for name in ("bad_dtype", "bad_shape"):
+        with pytest.raises(ValueError, match="requested dtype"):
+            cast(torch.ones(2), dtype=torch.bfloat16, rounding=name)
+    with pytest.raises(TypeError, match="return a tensor"):
+        cast(torch.ones(2), dtype=torch.bfloat16, rounding="not_tensor")
+    with pytest.raises(TypeError, match="float32"):
+        cast(torch.ones(2, dtype=torch.float64), dtype=torch.bfloat16)
+
+
+def test_builtin_casts_never_run_on_the_cpu():
+    """The built-in rules are the HIP kernels: a CPU tensor is an error, not a fallback."""
+    x = torch.ones(4)
+    assert cast(x, dtype=torch.float32) is x  # FP32 built-ins are the identity
+    for dtype in (torch.bfloat16, torch.float16, torch.float8_e4m3fn):
+        with pytest.raises(ValueError, match="GPU"):
+            cast(x, dtype=dtype, rounding="stochastic")
+    with pytest.raises(ValueError, match="GPU"):
+        sr_states.sr_cast_bf16(x, seed=1)
+
+
+@pytest.mark.parametrize("cls", CLASSES)
+def test_hip_optimizers_reject_reference_only_rules(cls):
+    """tests/test_rounding_registry.py:86-90."""
+    register_rounding("toward_zero", torch.bfloat16, reference=toward_zero)
+    with pytest.raises(ValueError, match="no HIP implementation"):
+        cls([torch.nn.Parameter(torch.ones(1))], lr=0.1, rounding="toward_zero")
+
+
+@pytest.mark.parametrize("cls", CLASSES)
+def test_group_overrides_and_checkpoints_require_registration(cls):
+    """tests/test_rounding_registry.py:93-110."""
+    p = torch.nn.Parameter(torch.ones(1))
+    with pytest.raises(ValueError, match="rounding"):
+        cls([{"params": [p], "rounding": "missing"}], lr=0.1)
+    optimizer = cls([p], lr=0.1)
+    with pytest.raises(ValueError, match="rounding"):
+        optimizer.add_param_group({"params": [torch.nn.Parameter(torch.ones(1))], "rounding": "missing"})
+    checkpoint = copy.deepcopy(optimizer.state_dict())
+    checkpoint["param_groups"][0]["state_format"][cls._state_names[0]]["rounding"] = "missing"
+    with pytest.raises(ValueError, match="rounding"):
+        optimizer.load_state_dict(checkpoint)
+    assert optimizer.param_groups[0]["state_format"][cls._state_names[0]]["rounding"] == "stochastic"
+
+
+# -- hyperparameter validation ----------------------------------------------------
+@pytest.mark.parametrize(
+    "kwargs",
+    [{"lr": -1}, {"lr": float("nan")}, {"eps": -1}, {"eps": float("inf")}, {"betas": (0.9, 1)},
+     {"betas": (float("nan"), 0.9)}, {"weight_decay": -1}, {"state_dtype": torch.int32},
+     {"rounding": "invalid"}, {"block_size": 64}],
+)
+def test_adamw_rejects_invalid_options(kwargs):
+    """tests/test_state_optimizers.py:110-127."""
+    with pytest.raises(ValueError):
+        AdamWHip([torch.nn.Parameter(torch.ones(1))], **kwargs)
+
+
+@pytest.mark.parametrize(
+    ("kwargs", "message"),
+    [({"lr": -0.1}, "learning rate"), ({"lr": 0.1, "momentum": 1.0}, "momentum value"),
+     ({"lr": 0.1, "rounding": "invalid"}, "rounding"), ({"lr": 0.1, "block_size": 64}, "block_size")],
+)
+def test_sgdm_rejects_invalid_options(kwargs, message):
+    """tests/test_triton_api.py:23-35."""
+    with pytest.raises(ValueError, match=message):
+        SGDMHip([torch.nn.Parameter(torch.ones(4))], **kwargs)
+
+
+# -- checkpoints -------------------------------------------------------------------
+@pytest.mark.parametrize("cls", CLASSES)
+@pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("parameter_dtype", [torch.float32, torch.bfloat16])
+def test_checkpoint_keeps_state_precision(cls, state_dtype, parameter_dtype):
+    """tests/test_state_optimizers.py:13-44."""
+    p = torch.nn.Parameter(torch.ones(4, dtype=parameter_dtype))
+    optimizer = cls([p], lr=0.01, state_dtype=state_dtype, seed=42)
+    original = torch.tensor([0.0, -0.0, 1.003125, 0.503125], dtype=state_dtype)
+    for name in optimizer._state_names:
+        optimizer.state[p][name] = original.clone()
+    if "exp_avg" in optimizer._state_names:
+        optimizer.state[p]["step"] = 7
+    optimizer.param_groups[0]["sr_step"] = 2**32 + 31
+    checkpoint = copy.deepcopy(optimizer.state_dict())
+    q = torch.nn.Parameter(p.detach().clone())
+    restored = cls([q], lr=0.3, state_dtype=torch.float32, seed=99)
+    seen = []
+    restored.register_load_state_dict_post_hook(lambda opt: seen.append(opt.state[q][opt._state_names[0]].dtype))
+    restored.load_state_dict(checkpoint)
+    assert seen == [state_dtype]
+    for name in optimizer._state_names:
+        actual = restored.state[q][name]
+        assert actual.dtype == state_dtype
+        assert torch.equal(bits(actual), bits(original))
+        assert actual.data_ptr() != checkpoint["state"][0][name].data_ptr()
+    assert restored.param_groups[0]["sr_step"] == 2**32 + 31
+    assert restored.param_groups[0]["sr_seed"] == 42
+    if "exp_avg" in optimizer._state_names:
+        assert restored.state[q]["step"] == 7
+
+
+def test_checkpoint_before_first_step_keeps_state_lazy():
+    """tests/test_triton_api.py:68-72."""
+    parameter = torch.nn.Parameter(torch.ones(4))
+    optimizer = SGDMHip([parameter], lr=0.1)
+    optimizer.load_state_dict(copy.deepcopy(optimizer.state_dict()))
+    assert not optimizer.state
+
+
+def test_bf16_state_survives_checkpoint_with_groups():
+    """tests/test_triton_api.py:38-65."""
+    source = torch.nn.Parameter(torch.ones(4))
+    unused = torch.nn.Parameter(torch.ones(4))
+    optimizer = SGDMHip([{"params": [source]}, {"params": [unused]}], lr=0.1, seed=44)
+    buffer = torch.tensor([0.0, -0.0, 1.0078125, -0.50390625], dtype=torch.bfloat16)
+    optimizer.state[source]["momentum_buffer"] = buffer.clone()
+    optimizer.param_groups[0]["sr_step"] = 2**32 + 17
+    checkpoint = copy.deepcopy(optimizer.state_dict())
+    target, target_unused = torch.nn.Parameter(torch.ones(4)), torch.nn.Parameter(torch.ones(4))
+    resumed = SGDMHip([{"params": [target]}, {"params": [target_unused]}], lr=0.9, seed=999)
+    resumed.load_state_dict(checkpoint)
+    restored = resumed.state[target]["momentum_buffer"]
+    assert restored.dtype == torch.bfloat16 and torch.equal(restored.view(torch.int16), buffer.view(torch.int16))
+    assert target_unused not in resumed.state
+    assert resumed.param_groups[0]["sr_step"] == 2**32 + 17
+    assert resumed.param_groups[1]["sr_step"] == 0
+    assert resumed.param_groups[0]["sr_seed"] == 44 and resumed.param_groups[0]["lr"] == 0.1
+
+
+def test_legacy_group_keys_are_migrated():
+    """tests/test_rng_streams.py:180-215 and tests/test_state_formats.py:168-175."""
+    p = torch.nn.Parameter(torch.ones(9, dtype=torch.bfloat16))
+    opt = AdamWHip([p], lr=0.01, seed=7)
+    opt.state[p]["exp_avg"] = torch.ones(9, dtype=torch.bfloat16)
+    opt.state[p]["exp_avg_sq"] = torch.ones(9, dtype=torch.bfloat16)
+    opt.state[p]["step"] = 2
+    checkpoint = copy.deepcopy(opt.state_dict())
+    group = checkpoint["param_groups"][0]
+    del group["sr_step"]
+    group["sr_offset"] = 2**32 + 29
+    resumed = AdamWHip([torch.nn.Parameter(p.detach().clone())], seed=3)
+    resumed.load_state_dict(checkpoint)
+    restored = resumed.param_groups[0]
+    assert restored["sr_step"] == 0 and restored["sr_seed"] == 7 and "sr_offset" not in restored
+    assert group["sr_offset"] == 2**32 + 29 and "sr_step" not in group  # caller's copy untouched
+    old = copy.deepcopy(checkpoint)
+    old["param_groups"][0].pop("state_format")
+    old["param_groups"][0].update(state_dtype=torch.float32, rounding="nearest")
+    resumed.load_state_dict(old)
+    q = resumed.param_groups[0]["params"][0]
+    assert all(resumed.state[q][n].dtype == torch.float32 for n in AdamWHip._state_names)
+    assert "state_format" not in old["param_groups"][0]
+
+
+@pytest.mark.parametrize("name", ["adamw_mixed", "adamw_minifloat", "sgdm_mixed"])
+def test_reference_checkpoints_load_into_hip_optimizers(name):
+    """A state_dict written by the reference's eager optimizer loads unchanged."""
+    case = torch.load(GOLDEN, weights_only=True)["cases"][name]
+    checkpoint = case["state_dict"]
+    stream = io.BytesIO()
+    torch.save(checkpoint, stream)
+    stream.seek(0)
+    checkpoint = torch.load(stream, weights_only=True)
+    dtypes = {"torch.float32": torch.float32, "torch.bfloat16": torch.bfloat16}
+    params = [torch.nn.Parameter(raw.view(dtypes[dt]).clone()) for raw, dt in zip(case["initial"], case["dtypes"])]
+    groups, at = [], 0
+    for group in case["groups"]:
+        groups.append({"params": params[at: at + len(group["sizes"])]})
+        at += len(group["sizes"])
+    cls = AdamWHip if case["kind"] == "adamw" else SGDMHip
+    opt = cls(groups, lr=0.5, seed=1)
+    opt.load_state_dict(checkpoint)
+    for group, saved in zip(opt.param_groups, checkpoint["param_groups"]):
+        assert group["sr_seed"] == saved["sr_seed"] and group["sr_step"] == saved["sr_step"]
+        assert group["state_format"] == saved["state_format"]
+        assert group["lr"] == saved["lr"]
+    last = case["steps"][-1]["states"]
+    for p, want in zip(params, last):
+        for state_name, value in want.items():
+            got = opt.state[p][state_name]
+            if isinstance(value, torch.Tensor):
+                assert torch.equal(bits(got), value)
+            else:
+                assert got == value
