@@ -255,3 +255,22 @@ def test_round_up_probability(dtype):
     result = sr_oracle.cast(torch.full((count,), value), dtype=dtype, seed=93, offset=2**32 - 41).float()
     freq = (result == hi).double().mean().item()
     assert abs(freq - p) < 6 * (p * (1 - p) / count) ** 0.5
+
+
+def test_oracle_bf16_neighbors_match_enumeration():
+    """sr_oracle.bf16_neighbors (sr_states/_bf16.py:77-101) against enumeration."""
+    gen = torch.Generator().manual_seed(5)
+    x = torch.cat([torch.randn(20_000, generator=gen) * 100, torch.tensor([1.5, -2.0, 0.0])])
+    lower, upper = sr_oracle.bf16_neighbors(x)
+    lo, hi = bf16_bracket(x)
+    assert torch.equal(lower.float(), lo) and torch.equal(upper.float(), hi)
+
+
+@pytest.mark.parametrize("dtype", MINIFLOATS)
+def test_oracle_minifloat_neighbors_match_enumerated_grid(dtype):
+    """sr_oracle.minifloat_neighbors (sr_states/_minifloat.py:73-99), tests/test_minifloat.py:94-100."""
+    x = boundary_inputs(dtype)
+    lower, upper = sr_oracle.minifloat_neighbors(x, dtype=dtype)
+    expected_lower, expected_upper = oracle_neighbors(x, dtype)
+    assert_bits_or_nan(lower, expected_lower.to(dtype))
+    assert_bits_or_nan(upper, expected_upper.to(dtype))
