@@ -54,11 +54,40 @@ WORKLOADS = {
         hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
         seed=7,
     ),
+    # Config 1: standalone SR cast of 2^24 FP32 values to BF16 (seed 7).  Eight
+    # input/output buffer pairs rotate so that 640 MB of traffic passes through
+    # the 256 MB last-level cache between reuses of a buffer.
+    "c1_cast_bf16": dict(
+        optimizer="cast",
+        shapes=[(1 << 24,)],
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=((torch.bfloat16, "stochastic"),),
+        grad_std=1.0,
+        hparams={},
+        seed=7,
+    ),
     "c2_single_2e26": dict(
         optimizer="adamw",
         shapes=[(1 << 26,)],
         p_dtype=torch.float32,
         g_dtype=torch.float32,
+        formats=((torch.bfloat16, "stochastic"), (torch.bfloat16, "stochastic")),
+        grad_std=1e-3,
+        hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
+        seed=7,
+    ),
+    # Config 3: GPT-2 small shapes (148 tensors, 124,439,808 elements), FP32
+    # parameters with BF16 gradients, BF16-SR moments
+    # (benchmarks/bench_optimizer_steps.py:33-53).
+    "c3_gpt2": dict(
+        optimizer="adamw",
+        shapes=[(50257, 768), (1024, 768)]
+        + [(768,), (768,), (768, 2304), (2304,), (768, 768), (768,), (768,), (768,),
+           (768, 3072), (3072,), (3072, 768), (768,)] * 12
+        + [(768,), (768,)],
+        p_dtype=torch.float32,
+        g_dtype=torch.bfloat16,
         formats=((torch.bfloat16, "stochastic"), (torch.bfloat16, "stochastic")),
         grad_std=1e-3,
         hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
@@ -103,6 +132,8 @@ def bytes_per_element(spec) -> int:
     size = lambda dt: torch.empty((), dtype=dt).element_size()  # noqa: E731
     if spec["optimizer"] == "copy":
         return 2 * size(spec["p_dtype"])
+    if spec["optimizer"] == "cast":
+        return size(spec["p_dtype"]) + size(spec["formats"][0][0])
     states = sum(2 * size(dt) for dt, _ in spec["formats"])
     return 2 * size(spec["p_dtype"]) + size(spec["g_dtype"]) + states
 
@@ -129,6 +160,20 @@ def build(spec, device):
         src = torch.empty(spec["shapes"][0], device=device).normal_(generator=gen)
         dst = torch.empty_like(src)
         return [src], lambda: dst.copy_(src)
+    if spec["optimizer"] == "cast":
+        from sr_states.hip.cast import native_cast
+
+        (dtype, rule), = spec["formats"]
+        inputs = [torch.empty(spec["shapes"][0], device=device).normal_(generator=gen) for _ in range(8)]
+        outputs = [torch.empty(spec["shapes"][0], device=device, dtype=dtype) for _ in range(8)]
+        turn = [0]
+        code = sr_states._lib.RULE_CODES[rule]
+
+        def cast_step():
+            k = turn[0] = (turn[0] + 1) % len(inputs)
+            native_cast(inputs[k], dtype=dtype, rule=code, seed=spec["seed"], out=outputs[k])
+
+        return inputs[:1], cast_step
     params = []
     for shape in spec["shapes"]:
         p = _Param(torch.empty(shape, device=device, dtype=spec["p_dtype"]))
@@ -158,8 +203,17 @@ def cpu_baseline(spec, target_seconds: float = 12.0):
     g = (torch.randn(n, generator=gen) * spec["grad_std"]).to(spec["g_dtype"])
     formats = tuple(sr_oracle.Fmt(d, r) for d, r in spec["formats"])
     group = {"params": [p], "grads": [g], "formats": formats, "sr_seed": spec["seed"], **spec["hparams"]}
-    cls = sr_oracle.AdamWOracle if spec["optimizer"] == "adamw" else sr_oracle.SGDMOracle
-    opt = cls([group])
+    if spec["optimizer"] == "cast":
+        (dtype, rule), = spec["formats"]
+
+        class _Cast:
+            def step(self):
+                sr_oracle.cast(p, dtype=dtype, rounding=rule, seed=spec["seed"])
+
+        opt = _Cast()
+    else:
+        cls = sr_oracle.AdamWOracle if spec["optimizer"] == "adamw" else sr_oracle.SGDMOracle
+        opt = cls([group])
     opt.step()  # allocate states
     times = []
     start = time.perf_counter()
@@ -192,7 +246,7 @@ def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--warmup", type=int, default=25)
     parser.add_argument("--workload", choices=sorted(WORKLOADS), default="north_star")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -238,6 +292,7 @@ def main():
             "adamw": "AdamW-SR step: params updated/sec and achieved HBM GB/s (% of peak), 1 MI355X",
             "sgdm": "SGDM-SR step: params updated/sec and achieved HBM GB/s (% of peak), 1 MI355X",
             "copy": "device copy (counter calibration): elements/sec, 1 MI355X",
+            "cast": "SR cast FP32->BF16: elements/sec and achieved HBM GB/s, 1 MI355X",
         }[spec["optimizer"]],
         "value": elements / (ms_per_step / 1e3),
         "unit": "params/s",

@@ -3,7 +3,9 @@
 Run ``python build.py`` from anywhere.  The AdamW instantiations are split
 into nine translation units (one per first-moment encoding) that compile in
 parallel; the shared library is linked in place next to the Python package,
-so it travels with the source tree.
+so it travels with the source tree.  The host-side group walk
+(csrc/group_walk.cpp, a CPython extension over torch's tensor type) is built
+alongside it as sr_states/_group_walk<EXT_SUFFIX>.
 """
 
 from __future__ import annotations
@@ -13,6 +15,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -23,6 +26,8 @@ OUTPUT = ROOT / "sr_states" / "libsr_states_hip.so"
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+WALK_OUTPUT = ROOT / "sr_states" / f"_group_walk{sysconfig.get_config_var('EXT_SUFFIX')}"
 
 # -ffp-contract=off: only the explicit fmaf() calls may fuse, matching the
 # eager CPU reference.  Division and sqrt stay IEEE correctly rounded.
@@ -52,6 +57,33 @@ def units() -> list[tuple[Path, list[str], Path]]:
     return jobs
 
 
+def walk_command(output: Path) -> list[str]:
+    """g++ line for the group-walk extension, against the running torch."""
+    import torch.utils.cpp_extension as ext
+
+    torch_lib = ext.library_paths()[0]
+    return [
+        CXX,
+        "-O2",
+        "-std=c++17",
+        "-shared",
+        "-fPIC",
+        "-Wall",
+        f"-D_GLIBCXX_USE_CXX11_ABI={int(__import__('torch')._C._GLIBCXX_USE_CXX11_ABI)}",
+        f"-I{sysconfig.get_paths()['include']}",
+        *(f"-I{path}" for path in ext.include_paths()),
+        str(CSRC / "group_walk.cpp"),
+        "-o",
+        str(output),
+        f"-L{torch_lib}",
+        "-lc10",
+        "-ltorch",
+        "-ltorch_cpu",
+        "-ltorch_python",
+        f"-Wl,-rpath,{torch_lib}",
+    ]
+
+
 def _run(cmd: list[str]) -> None:
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
@@ -71,6 +103,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
         [HIPCC, *HIP_FLAGS, *defines, "-c", str(src), "-o", str(obj)]
         for src, defines, obj in units()
     ]
+    walk_tmp = WALK_OUTPUT.with_name(WALK_OUTPUT.name + ".tmp")
+    commands.append(walk_command(walk_tmp))
     workers = jobs or min(len(commands), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(workers) as pool:
         for cmd, _ in zip(commands, pool.map(_run, commands)):
@@ -81,6 +115,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     link += [str(obj) for _, _, obj in units()]
     _run(link)
     os.replace(tmp, OUTPUT)
+    os.replace(walk_tmp, WALK_OUTPUT)
     return OUTPUT
 
 

@@ -181,33 +181,23 @@ class AdamWHip(StateOptimizer):
         )
 
     def _step_group(self, group, formats, items, rng_step):
-        items = list(items)
-        if not items:
-            return
-        launches = prepare_group(self, group, formats, items, validate_update_device)
+        launches, record_steps = prepare_group(
+            self, group, formats, items, validate_update_device
+        )
         beta1, beta2 = group["betas"]
         (m_code, m_rule), (v_code, v_rule) = (native_codes(f.dtype, f.rounding) for f in formats)
         seed, rng_word = _lib.low64(group["sr_seed"]), _lib.low64(rng_step)
         block_size = self._group_block_size(group)
-        for device, step, rows, tables in launches:
+        for device, step, codes, tables in launches:
             hparams = adamw_hparams(
                 group["lr"], beta1, beta2, group["eps"], group["weight_decay"], step
             )
-            parameter, gradient = rows[0].tensors[:2]
-            dtypes = (
-                _lib.DTYPE_CODES[parameter.dtype],
-                _lib.DTYPE_CODES[gradient.dtype],
-                m_code,
-                m_rule,
-                v_code,
-                v_rule,
-            )
+            dtypes = (*codes, m_code, m_rule, v_code, v_rule)
             with torch.cuda.device(device):
                 _launch(
                     tables, dtypes, hparams, seed, rng_word, block_size, _lib.stream_handle(device)
                 )
-        for _, state, _, step, _ in items:
-            state["step"] = step
+        record_steps()
 
 
 class AdamWHipRN(AdamWHip):

@@ -22,12 +22,21 @@ CAST_STORE_MODES = ("convert", "bits")
 _DEFAULT_THREADS = 256
 
 
-def native_cast(x, *, dtype, rule, seed=0, offset=0, threads=_DEFAULT_THREADS):
-    """Cast contiguous FP32 ``x`` with HIP rule code ``rule``; returns a new tensor."""
+def native_cast(x, *, dtype, rule, seed=0, offset=0, threads=_DEFAULT_THREADS, out=None):
+    """Cast contiguous FP32 ``x`` with HIP rule code ``rule``.
+
+    Returns a new tensor, or writes into ``out`` (contiguous, ``dtype``, x's
+    shape and device, disjoint from x) when given.
+    """
     if x.device.type != "cuda":
         raise ValueError(f"sr_states casts run on the GPU; got a {x.device.type} tensor")
     validate_device(x.device)
-    output = torch.empty(x.shape, dtype=dtype, device=x.device)
+    if out is None:
+        output = torch.empty(x.shape, dtype=dtype, device=x.device)
+    else:
+        if out.dtype != dtype or out.shape != x.shape or out.device != x.device or not out.is_contiguous():
+            raise ValueError("out must be a contiguous tensor of the requested dtype, shape and device")
+        output = out
     if x.numel():
         with torch.cuda.device(x.device):
             _lib.call(

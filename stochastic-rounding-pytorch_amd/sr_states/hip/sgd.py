@@ -148,21 +148,25 @@ class SGDMHip(StateOptimizer):
         )
 
     def _step_group(self, group, formats, items, rng_step):
-        items = list(items)
-        if not items:
-            return
-        launches = prepare_group(self, group, formats, items, validate_update_device)
+        launches, record_steps = prepare_group(
+            self, group, formats, items, validate_update_device
+        )
         code, rule = native_codes(formats[0].dtype, formats[0].rounding)
         hparams = sgdm_hparams(group["lr"], group["momentum"])
         seed, rng_word = _lib.low64(group["sr_seed"]), _lib.low64(rng_step)
         block_size = self._group_block_size(group)
-        for device, _, rows, tables in launches:
-            parameter, gradient = rows[0].tensors[:2]
-            dtypes = (_lib.DTYPE_CODES[parameter.dtype], _lib.DTYPE_CODES[gradient.dtype], code, rule)
+        for device, _, codes, tables in launches:
             with torch.cuda.device(device):
                 _launch(
-                    tables, dtypes, hparams, seed, rng_word, block_size, _lib.stream_handle(device)
+                    tables,
+                    (*codes, code, rule),
+                    hparams,
+                    seed,
+                    rng_word,
+                    block_size,
+                    _lib.stream_handle(device),
                 )
+        record_steps()
 
 
 class SGDMHipRN(SGDMHip):

@@ -23,8 +23,9 @@ for path in (ROOT, PACKAGE_DIR):
 
 def pytest_configure(config):
     # Markers are registered in pytest.ini.
+    built = (PACKAGE_DIR / "sr_states").glob("_group_walk*.so")
     library = PACKAGE_DIR / "sr_states" / "libsr_states_hip.so"
-    if not library.exists() and not torch.cuda.is_available():
+    if (not library.exists() or not any(built)) and not torch.cuda.is_available():
         # Only a CPU checkout builds here; GPU runs use the prebuilt library.
         import importlib.util
 

@@ -1,0 +1,286 @@
+"""The native group signature and the steady-state reuse of validated launches.
+
+The reference validates and rebuilds every bucket on each step
+(sr_states/triton/_multi_tensor.py:22-134).  This backend reuses the last
+validated step's launches when the native signature of the group is
+unchanged; these tests pin that every fact the validation or the tables
+depend on changes the signature, that anything it cannot vouch for takes the
+validating path, and that reused steps launch and record exactly what the
+validating path would.  The kernel launch is replaced by a recorder.
+"""
+
+from __future__ import annotations
+
+import copy
+import importlib
+from contextlib import nullcontext
+
+import pytest
+import torch
+
+from sr_states import AdamWHip, SGDMHip, _group_walk, _lib
+from sr_states.hip import _multi_tensor
+
+NAMES = ("exp_avg", "exp_avg_sq")
+
+
+def _group(n=3, size=5):
+    params = [torch.nn.Parameter(torch.zeros(size)) for _ in range(n)]
+    state = {}
+    for p in params:
+        p.grad = torch.zeros(size)
+        state[p] = {name: torch.zeros(size, dtype=torch.bfloat16) for name in NAMES}
+    return params, state
+
+
+def _sig(params, state, *, uses_step=True, first_index=0):
+    return _group_walk.group_signature(params, state, NAMES, uses_step, first_index)
+
+
+def test_signature_is_stable_and_lists_state_entries():
+    params, state = _group()
+    first, second = _sig(params, state), _sig(params, state)
+    assert first[0] == second[0] and first[1] == 0
+    assert first[2] == [state[p] for p in params]
+    assert _sig(params, state, first_index=3)[0] != first[0]
+
+
+@pytest.mark.parametrize(
+    "change",
+    [
+        "grad_address", "grad_none", "state_shape", "state_dtype", "state_noncontiguous",
+        "param_storage_offset", "grad_dtype", "step", "state_type",
+    ],
+)
+def test_every_table_input_changes_the_signature(change):
+    params, state = _group()
+    before = _sig(params, state)
+    p = params[1]
+    if change == "grad_address":
+        p.grad = torch.zeros(5)
+    elif change == "grad_none":
+        p.grad = None
+    elif change == "state_shape":
+        state[p]["exp_avg"] = torch.zeros(1, 5, dtype=torch.bfloat16)
+    elif change == "state_dtype":
+        state[p]["exp_avg"] = torch.zeros(5, dtype=torch.float16)
+    elif change == "state_noncontiguous":
+        state[p]["exp_avg"] = torch.zeros(10, dtype=torch.bfloat16)[::2]
+    elif change == "param_storage_offset":
+        p.data = torch.zeros(6)[1:]
+    elif change == "grad_dtype":
+        p.grad = None
+        p.data = p.data.bfloat16()
+        p.grad = torch.zeros(5, dtype=torch.bfloat16)
+    elif change == "step":
+        for q in params:
+            state[q]["step"] = 1
+    elif change == "state_type":
+        class Sub(torch.Tensor):
+            pass
+        state[p]["exp_avg"] = state[p]["exp_avg"].as_subclass(Sub)
+    after = _sig(params, state)
+    assert after is not None and (after[0] != before[0] or after[1] != before[1])
+
+
+def test_in_place_resize_keeps_the_address_but_changes_the_signature():
+    params, state = _group()
+    before = _sig(params, state)
+    state[params[0]]["exp_avg_sq"].resize_(4)
+    assert _sig(params, state)[0] != before[0]
+
+
+class _Wrapper(torch.Tensor):
+    """Tensor subclass whose data lives elsewhere (as DTensor's does)."""
+
+    @staticmethod
+    def __new__(cls, elem):
+        return torch.Tensor._make_wrapper_subclass(cls, elem.shape, dtype=elem.dtype)
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        raise NotImplementedError(func)
+
+
+@pytest.mark.parametrize("case", ["missing_state", "missing_name", "tensor_step", "mixed_steps",
+                                  "wrapper", "meta", "not_a_tensor", "sparse_grad",
+                                  "no_gradients", "huge_step"])
+def test_unvouched_groups_take_the_validating_path(case):
+    params, state = _group()
+    p = params[0]
+    if case == "missing_state":
+        del state[p]
+    elif case == "missing_name":
+        del state[p]["exp_avg"]
+    elif case == "tensor_step":
+        for q in params:
+            state[q]["step"] = torch.tensor(1.0)
+    elif case == "mixed_steps":
+        state[p]["step"] = 2
+    elif case == "wrapper":
+        state[p]["exp_avg"] = _Wrapper(state[p]["exp_avg"])
+    elif case == "meta":
+        moved = torch.nn.Parameter(torch.zeros(5, device="meta"))
+        moved.grad = torch.zeros(5, device="meta")
+        state[moved] = {name: torch.zeros(5, dtype=torch.bfloat16, device="meta") for name in NAMES}
+        params[1] = moved
+    elif case == "not_a_tensor":
+        state[p]["exp_avg"] = 0.0
+    elif case == "sparse_grad":
+        p.grad = torch.sparse_coo_tensor([[0]], [1.0], (5,))
+    elif case == "no_gradients":
+        for q in params:
+            q.grad = None
+    elif case == "huge_step":
+        for q in params:
+            state[q]["step"] = 1 << 70
+    assert _sig(params, state) is None
+
+
+def test_set_steps_writes_every_entry():
+    entries = [{}, {"step": 3}]
+    _group_walk.set_steps(entries, 7)
+    assert entries == [{"step": 7}, {"step": 7}]
+    with pytest.raises(TypeError):
+        _group_walk.set_steps([1], 1)
+
+
+# -- the optimizers' steady-state path ----------------------------------------------
+@pytest.fixture
+def recorder(monkeypatch):
+    launches = []
+    for kind in ("adamw", "sgd"):
+        module = importlib.import_module(f"sr_states.hip.{kind}")
+
+        def record(tables, dtypes, hparams, seed, rng_step, block_size, stream, _kind=kind):
+            launches.append({"kind": _kind, "tables": tables, "dtypes": dtypes, "hparams": hparams,
+                             "seed": seed, "rng_step": rng_step, "block_size": block_size})
+
+        monkeypatch.setattr(module, "_launch", record)
+        monkeypatch.setattr(module, "validate_update_device", lambda *args: None)
+    monkeypatch.setattr(torch.cuda, "device", lambda device: nullcontext())
+    monkeypatch.setattr(_lib, "stream_handle", lambda device: 0)
+    return launches
+
+
+def _spy(monkeypatch):
+    calls = []
+    real = _multi_tensor.bucket_items
+
+    def counting(*args, **kwargs):
+        calls.append(1)
+        return real(*args, **kwargs)
+
+    monkeypatch.setattr(_multi_tensor, "bucket_items", counting)
+    return calls
+
+
+def test_steady_steps_reuse_tables_and_record_steps(recorder, monkeypatch):
+    validations = _spy(monkeypatch)
+    params = [torch.nn.Parameter(torch.ones(n)) for n in (3, 1100, 7)]
+    opt = AdamWHip([{"params": params[:2]}, {"params": params[2:]}], lr=0.01, seed=5)
+    for p in params:
+        p.grad = torch.ones_like(p)
+    for _ in range(4):
+        opt.step()
+    # Step 1 allocates states (no signature yet), step 2 validates and records
+    # the plan; steps 3 and 4 reuse it.
+    assert len(validations) == 4
+    first_group = [launch for launch in recorder if launch["tables"].nrows == 2]
+    assert len({id(launch["tables"]) for launch in first_group}) == 1
+    assert [launch["rng_step"] for launch in first_group] == [1, 2, 3, 4]
+    assert [launch["hparams"].neg_step_size for launch in first_group] == [
+        pytest.approx(-0.01 / (1 - 0.9**t)) for t in (1, 2, 3, 4)]
+    assert [opt.state[p]["step"] for p in params] == [4, 4, 4]
+    assert recorder[-1]["tables"].records["param_index"].tolist() == [2]
+
+
+def test_changes_after_reuse_are_validated_again(recorder, monkeypatch):
+    validations = _spy(monkeypatch)
+    params = [torch.nn.Parameter(torch.ones(9)) for _ in range(3)]
+    opt = AdamWHip(params, lr=0.01)
+    for p in params:
+        p.grad = torch.ones_like(p)
+    for _ in range(3):
+        opt.step()
+    assert len(validations) == 2
+    # A new gradient tensor moves an address: the tables are rebuilt.
+    params[1].grad = torch.full_like(params[1], 2.0)
+    opt.step()
+    assert len(validations) == 3
+    records = recorder[-1]["tables"].records
+    assert int(records["ptr"][1][1]) == params[1].grad.data_ptr()
+    # A parameter without a gradient keeps its index but leaves the bucket.
+    params[0].grad = None
+    opt.step()
+    assert recorder[-1]["tables"].records["param_index"].tolist() == [1, 2]
+    assert [opt.state[p]["step"] for p in params] == [4, 5, 5]
+    # Mixed stored steps split the bucket again, through the validating path.
+    params[0].grad = torch.ones(9)
+    opt.step()
+    assert [launch["tables"].nrows for launch in recorder[-2:]] == [1, 2]
+    assert [launch["hparams"].neg_step_size for launch in recorder[-2:]] == [
+        pytest.approx(-0.01 / (1 - 0.9**t)) for t in (5, 6)]
+    # An in-place resize keeps the address; the shape check still fires.
+    opt.step()
+    opt.state[params[2]]["exp_avg"].resize_(3, 3)
+    count = len(recorder)
+    with pytest.raises(ValueError, match="shapes"):
+        opt.step()
+    assert len(recorder) == count
+
+
+def test_reuse_still_validates_hyperparameters(recorder):
+    p = torch.nn.Parameter(torch.ones(4))
+    opt = SGDMHip([p], lr=0.01, momentum=0.9)
+    p.grad = torch.ones_like(p)
+    for _ in range(3):
+        opt.step()
+    count = len(recorder)
+    opt.param_groups[0]["lr"] = -1.0
+    with pytest.raises(ValueError, match="learning rate"):
+        opt.step()
+    assert len(recorder) == count
+    opt.param_groups[0]["lr"] = 0.5
+    opt.step()
+    assert recorder[-1]["hparams"].neg_lr == pytest.approx(-0.5)
+
+
+def test_format_and_block_size_changes_invalidate_the_plan(recorder):
+    p = torch.nn.Parameter(torch.ones(4))
+    opt = AdamWHip([p], lr=0.01, block_size=256)
+    p.grad = torch.ones_like(p)
+    for _ in range(3):
+        opt.step()
+    opt.param_groups[0]["block_size"] = 512
+    opt.step()
+    assert recorder[-1]["block_size"] == 512
+    assert recorder[-1]["tables"] is not recorder[-2]["tables"]
+    # Switching the stored dtype through state_format fails the state check.
+    opt.param_groups[0]["state_format"] = {"exp_avg": {"dtype": torch.float16, "rounding": "stochastic"},
+                                           "exp_avg_sq": {"dtype": torch.bfloat16, "rounding": "stochastic"}}
+    with pytest.raises(ValueError, match="dtype does not match"):
+        opt.step()
+
+
+def test_checkpoint_round_trip_with_reuse_matches_fresh_validation(recorder):
+    """Resuming replaces every state tensor: the first resumed step validates."""
+    params = [torch.nn.Parameter(torch.linspace(-1, 1, 17)) for _ in range(2)]
+    opt = AdamWHip(params, lr=0.1, seed=4)
+    for _ in range(3):
+        for p in params:
+            p.grad = torch.ones_like(p)
+        opt.step()
+    clones = [torch.nn.Parameter(p.detach().clone()) for p in params]
+    for c in clones:
+        c.grad = torch.ones_like(c)
+    resumed = AdamWHip(clones, lr=0.1)
+    resumed.load_state_dict(copy.deepcopy(opt.state_dict()))
+    recorder.clear()
+    resumed.step()
+    opt.step()
+    first, second = recorder
+    assert first["rng_step"] == second["rng_step"] == 4
+    assert first["seed"] == second["seed"] == 4
+    assert first["hparams"].neg_step_size == second["hparams"].neg_step_size
+    assert first["tables"].records["param_index"].tolist() == [0, 1]
