@@ -93,6 +93,9 @@ WORKLOADS = {
         hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
         seed=7,
     ),
+    # Config 4: E4M3-SR first moment, BF16-SR second moment over the 1.5 G
+    # element set; gradients carry values beyond +-448/(1-beta1) and +-Inf so
+    # that the saturating E4M3 encoder is exercised.
     "c4_fp8_mixed": dict(
         optimizer="adamw",
         shapes=C4_BLOCK * 7 + [(32000, 4096)],
@@ -100,6 +103,20 @@ WORKLOADS = {
         g_dtype=torch.float32,
         formats=((torch.float8_e4m3fn, "stochastic"), (torch.bfloat16, "stochastic")),
         grad_std=1e-3,
+        special="saturate",
+        hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
+        seed=7,
+    ),
+    # Config 4 at its literal size: 24 blocks plus the embedding, 4.99 G
+    # elements (55 GB of parameters, gradients and moments).
+    "c4_fp8_24block": dict(
+        optimizer="adamw",
+        shapes=C4_BLOCK * 24 + [(32000, 4096)],
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=((torch.float8_e4m3fn, "stochastic"), (torch.bfloat16, "stochastic")),
+        grad_std=1e-3,
+        special="saturate",
         hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
         seed=7,
     ),
@@ -115,6 +132,8 @@ WORKLOADS = {
         hparams={},
         seed=0,
     ),
+    # Config 5: gradients with 5% exact zeros, 1% of magnitude below 2^-14
+    # (FP16 subnormal range) and the rest N(0, 1e-2).
     "c5_sgdm_fp16": dict(
         optimizer="sgdm",
         shapes=[(2048, 2048)] * 256,
@@ -122,6 +141,7 @@ WORKLOADS = {
         g_dtype=torch.float32,
         formats=((torch.float16, "stochastic"),),
         grad_std=1e-2,
+        special="zeros_subnormal",
         hparams=dict(lr=0.1, momentum=0.9),
         seed=11,
     ),
@@ -150,10 +170,50 @@ class _Param(torch.nn.Parameter):
         self._gradient = value
 
 
+def make_gradient(shape, spec, gen, device):
+    """FP32 gradient of one tensor of a workload, with the config's special values."""
+    g = torch.empty(shape, device=device, dtype=torch.float32).normal_(
+        std=spec["grad_std"], generator=gen
+    )
+    flat = g.view(-1)
+    special = spec.get("special")
+    if special == "saturate":
+        # |g| = 5000 makes |m'| = 500 > 448 at the first step.
+        flat[5::997] = 5000.0
+        flat[500::1994] = -5000.0
+        flat[11::1_000_003] = float("inf")
+        flat[600_011::1_000_003] = float("-inf")
+    elif special == "zeros_subnormal":
+        u = torch.rand(flat.shape, device=device, generator=gen)
+        tiny = (torch.rand(flat.shape, device=device, generator=gen) * 2 - 1) * 2.0**-14
+        flat.copy_(torch.where(u < 0.05, 0.0, torch.where(u < 0.06, tiny, flat)))
+    elif special is not None:
+        raise ValueError(f"unknown special gradient values {special!r}")
+    return g
+
+
+def make_optimizer(spec, device):
+    """(parameters, optimizer) of an optimizer workload, inputs resident on `device`."""
+    import sr_states
+    from sr_states import StateFormat
+
+    gen = torch.Generator(device=device).manual_seed(spec["seed"])
+    params = []
+    for shape in spec["shapes"]:
+        p = _Param(torch.empty(shape, device=device, dtype=spec["p_dtype"]))
+        with torch.no_grad():
+            p.normal_(std=0.02, generator=gen)
+        p.grad = make_gradient(shape, spec, gen, device).to(spec["g_dtype"])
+        params.append(p)
+    names = ("exp_avg", "exp_avg_sq") if spec["optimizer"] == "adamw" else ("momentum_buffer",)
+    formats = {n: StateFormat(d, r) for n, (d, r) in zip(names, spec["formats"])}
+    cls = sr_states.AdamWHip if spec["optimizer"] == "adamw" else sr_states.SGDMHip
+    return params, cls(params, state_format=formats, seed=spec["seed"], **spec["hparams"])
+
+
 def build(spec, device):
     """(tensors, step callable) of a workload, inputs resident on `device`."""
     import sr_states
-    from sr_states import StateFormat
 
     gen = torch.Generator(device=device).manual_seed(spec["seed"])
     if spec["optimizer"] == "copy":
@@ -174,62 +234,69 @@ def build(spec, device):
             native_cast(inputs[k], dtype=dtype, rule=code, seed=spec["seed"], out=outputs[k])
 
         return inputs[:1], cast_step
-    params = []
-    for shape in spec["shapes"]:
-        p = _Param(torch.empty(shape, device=device, dtype=spec["p_dtype"]))
-        with torch.no_grad():
-            p.normal_(std=0.02, generator=gen)
-        g = torch.empty(shape, device=device, dtype=torch.float32).normal_(std=spec["grad_std"], generator=gen)
-        p.grad = g.to(spec["g_dtype"])
-        params.append(p)
-    names = ("exp_avg", "exp_avg_sq") if spec["optimizer"] == "adamw" else ("momentum_buffer",)
-    formats = {n: StateFormat(d, r) for n, (d, r) in zip(names, spec["formats"])}
-    if spec["optimizer"] == "adamw":
-        opt = sr_states.AdamWHip(params, state_format=formats, seed=spec["seed"], **spec["hparams"])
-    else:
-        opt = sr_states.SGDMHip(params, state_format=formats, seed=spec["seed"], **spec["hparams"])
+    params, opt = make_optimizer(spec, device)
     return params, opt.step
 
 
+def _median_step_seconds(opt, target_seconds: float, min_steps: int = 3) -> tuple[float, int]:
+    opt.step()  # allocate states
+    times = []
+    start = time.perf_counter()
+    while time.perf_counter() - start < target_seconds or len(times) < min_steps:
+        t0 = time.perf_counter_ns()
+        opt.step()
+        times.append((time.perf_counter_ns() - t0) / 1e9)
+    return sorted(times)[len(times) // 2], len(times)
+
+
 def cpu_baseline(spec, target_seconds: float = 12.0):
-    """Time the eager CPU path (oracle restatement) on one tensor of the workload."""
+    """Time the eager CPU path (oracle restatement) on one tensor of the workload.
+
+    Two thirds of the budget go to torch's default thread count, the rest to
+    one thread on a quarter-size sample.
+    """
     sys.path.insert(0, str(ROOT))
     from oracle import sr_oracle
 
     shape = max(spec["shapes"], key=lambda s: math.prod(s))
     n = min(math.prod(shape), 1 << 24)
-    gen = torch.Generator().manual_seed(spec["seed"])
-    p = (torch.randn(n, generator=gen) * 0.02).to(spec["p_dtype"])
-    g = (torch.randn(n, generator=gen) * spec["grad_std"]).to(spec["g_dtype"])
-    formats = tuple(sr_oracle.Fmt(d, r) for d, r in spec["formats"])
-    group = {"params": [p], "grads": [g], "formats": formats, "sr_seed": spec["seed"], **spec["hparams"]}
-    if spec["optimizer"] == "cast":
-        (dtype, rule), = spec["formats"]
 
-        class _Cast:
-            def step(self):
-                sr_oracle.cast(p, dtype=dtype, rounding=rule, seed=spec["seed"])
+    def make(count):
+        gen = torch.Generator().manual_seed(spec["seed"])
+        p = (torch.randn(count, generator=gen) * 0.02).to(spec["p_dtype"])
+        g = make_gradient((count,), spec, gen, "cpu").to(spec["g_dtype"])
+        if spec["optimizer"] == "cast":
+            (dtype, rule), = spec["formats"]
 
-        opt = _Cast()
-    else:
+            class _Cast:
+                def step(self):
+                    sr_oracle.cast(p, dtype=dtype, rounding=rule, seed=spec["seed"])
+
+            return _Cast()
+        formats = tuple(sr_oracle.Fmt(d, r) for d, r in spec["formats"])
+        group = {"params": [p], "grads": [g], "formats": formats, "sr_seed": spec["seed"],
+                 **spec["hparams"]}
         cls = sr_oracle.AdamWOracle if spec["optimizer"] == "adamw" else sr_oracle.SGDMOracle
-        opt = cls([group])
-    opt.step()  # allocate states
-    times = []
-    start = time.perf_counter()
-    while time.perf_counter() - start < target_seconds or len(times) < 3:
-        t0 = time.perf_counter_ns()
-        opt.step()
-        times.append((time.perf_counter_ns() - t0) / 1e9)
-    median = sorted(times)[len(times) // 2]
+        return cls([group])
+
+    threads = torch.get_num_threads()
+    median, count = _median_step_seconds(make(n), target_seconds * 2 / 3)
+    n1 = max(n // 4, 1)
+    torch.set_num_threads(1)
+    try:
+        median1, count1 = _median_step_seconds(make(n1), target_seconds / 3)
+    finally:
+        torch.set_num_threads(threads)
     return {
         "value": n / median,
         "unit": "params/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
         "kind": "port",
-        "sample": f"{len(times)} eager steps of one {n}-element tensor of the workload "
-        f"(torch {torch.__version__}, {torch.backends.cpu.get_cpu_capability()}, "
-        f"{os.cpu_count()} host CPUs visible), median step {median * 1e3:.1f} ms",
+        "value_one_thread": n1 / median1,
+        "sample": f"{count} eager steps of one {n}-element tensor of the workload at {threads} "
+        f"threads (median {median * 1e3:.1f} ms) and {count1} steps of {n1} elements at 1 thread "
+        f"(median {median1 * 1e3:.1f} ms); torch {torch.__version__}, "
+        f"{torch.backends.cpu.get_cpu_capability()}, {os.cpu_count()} host CPUs visible",
     }
 
 
@@ -245,7 +312,7 @@ def load_traffic(workload: str):
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--steps", type=int, default=100)
     parser.add_argument("--warmup", type=int, default=25)
     parser.add_argument("--workload", choices=sorted(WORKLOADS), default="north_star")
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -279,7 +346,8 @@ def main():
     total_end.record()
     torch.cuda.synchronize()
     total_ms = total_start.elapsed_time(total_end)
-    kernel_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / args.steps
+    step_ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    kernel_ms = sum(step_ms) / args.steps
     ms_per_step = total_ms / args.steps
 
     bpe = bytes_per_element(spec)
@@ -324,6 +392,7 @@ def main():
             "frac": achieved / HBM_PEAK_GBPS,
             "traffic": traffic,
             "kernel_ms": kernel_ms,
+            "kernel_ms_median": step_ms[len(step_ms) // 2],
             "algorithmic_bytes_per_launch": bytes_per_launch,
         },
         "cpu_baseline": None,
