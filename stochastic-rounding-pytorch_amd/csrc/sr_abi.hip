@@ -74,10 +74,11 @@ int pg_index(int dtype) { return dtype == SR_F32 ? 0 : (dtype == SR_BF16 ? 1 : -
 
 bool valid_block(int block) { return block >= 64 && block <= sr::kMaxBlock && block % 64 == 0; }
 
-// One workgroup per tile; the grid is padded to a multiple of the XCD count
-// so that the XCD-contiguous tile order of the kernels is a permutation.
+// One workgroup per tile; the grid is padded to a whole number of XCD chunk
+// rounds so that the kernels' tile order (sr_tile_order.h) is a permutation.
+// `tiles` must equal the total_tiles the kernel argument carries.
 int launch(const void* fn, int block, uint32_t tiles, void* arg, void* stream) {
-  const uint64_t grid = (static_cast<uint64_t>(tiles) + sr::kXcds - 1) / sr::kXcds * sr::kXcds;
+  const uint64_t grid = sr::padded_grid(tiles);
   if (grid > 0x7FFFFFFFull) return fail(SR_ERR_ARGUMENT, "%u tiles exceed the grid limit", tiles);
   void* args[] = {arg};
   hipError_t err = hipLaunchKernel(fn, dim3(static_cast<unsigned>(grid)), dim3(block), args, 0,

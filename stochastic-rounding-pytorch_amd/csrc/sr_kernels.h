@@ -9,12 +9,11 @@
 // aligned, and the partial last tile of a row, take a coalesced scalar path
 // (element k*blockDim.x + lane of the tile).
 //
-// XCD-aware order.  The dispatcher hands workgroup b to XCD (b mod 8).  The
-// logical tile of workgroup b is (b mod 8) * G/8 + b/8 (G = padded grid), so
-// each XCD streams one contiguous eighth of the tile space and the
-// concurrently active tiles of an XCD stay close together.  Measured on
-// MI355X for the 12-byte-read / 8-byte-write pattern of the fused update,
-// this order and one tile per workgroup beat persistent grid-stride loops.
+// XCD-aware order.  Workgroups map to tiles through sr_tile_order.h: each
+// XCD takes chunks of up to 512 consecutive tiles in turn, so the tiles in
+// flight on one XCD stay close together.  Measured on MI355X for the
+// 12-byte-read / 8-byte-write pattern of the fused update, this order and one
+// tile per workgroup beat persistent grid-stride loops.
 //
 // Multi-tensor launches.  `tile_rows[t]` names the row (tensor) of tile t
 // and `rows[row]` is its 64-byte sr_row record: both are read once per
@@ -27,13 +26,13 @@
 
 #include "../../include/sr_states_hip.h"
 #include "sr_math.h"
+#include "sr_tile_order.h"
 
 namespace sr {
 
 constexpr int kEpt = SR_ELEMENTS_PER_THREAD;
 static_assert(kEpt == 2 || kEpt == 4 || kEpt == 8, "lanes move 2, 4 or 8 elements");
 constexpr int kMaxBlock = 1024;
-constexpr uint32_t kXcds = 8;
 
 struct AdamWArgs {
   const sr_row* rows;        // device table; nullptr selects `inline_row`
@@ -62,10 +61,10 @@ struct CastArgs {
   uint32_t vector_ok;     // x and y 16-byte aligned
 };
 
-// Logical tile of this workgroup; >= total for the padding workgroups.
-__device__ __forceinline__ uint32_t logical_tile() {
-  const uint32_t per_xcd = gridDim.x / kXcds;  // the host pads the grid to a multiple of 8
-  return (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+// Logical tile of this workgroup; >= total_tiles for the padding workgroups.
+// The host launches padded_grid(total_tiles) workgroups.
+__device__ __forceinline__ uint32_t logical_tile(uint32_t total_tiles) {
+  return tile_of(blockIdx.x, total_tiles);
 }
 
 // ---------------------------------------------------------------------------
@@ -214,7 +213,7 @@ __device__ __forceinline__ void adamw_scalar(char* p, const char* g, char* m, ch
 
 template <int PE, int GE, int ME, int VE>
 __global__ __launch_bounds__(kMaxBlock) void adamw_kernel(const AdamWArgs a) {
-  const uint32_t t = logical_tile();
+  const uint32_t t = logical_tile(a.total_tiles);
   if (t >= a.total_tiles) return;
   const sr_row& r = tile_row(a, t);
   char* p = reinterpret_cast<char*>(r.ptr[0]);
@@ -273,7 +272,7 @@ __device__ __forceinline__ void sgdm_scalar(char* p, const char* g, char* u, int
 
 template <int PE, int GE, int UE>
 __global__ __launch_bounds__(kMaxBlock) void sgdm_kernel(const SgdmArgs a) {
-  const uint32_t t = logical_tile();
+  const uint32_t t = logical_tile(a.total_tiles);
   if (t >= a.total_tiles) return;
   const sr_row& r = tile_row(a, t);
   char* p = reinterpret_cast<char*>(r.ptr[0]);
@@ -299,7 +298,7 @@ __global__ __launch_bounds__(kMaxBlock) void sgdm_kernel(const SgdmArgs a) {
 // ---------------------------------------------------------------------------
 template <int ENC>
 __global__ __launch_bounds__(kMaxBlock) void cast_kernel(const CastArgs a) {
-  const uint32_t t = logical_tile();
+  const uint32_t t = logical_tile(a.total_tiles);
   if (t >= a.total_tiles) return;
   const uint32_t tile = blockDim.x * kEpt;
   const int64_t start = static_cast<int64_t>(t) * tile;
