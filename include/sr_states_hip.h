@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SR_ABI_VERSION 2
+#define SR_ABI_VERSION 3
 
 /* Storage dtypes (torch.float32, bfloat16, float16, float8_e4m3fn,
  * float8_e5m2).  The set mirrors the built-in rounding table of the
@@ -54,10 +54,14 @@ enum sr_error {
   SR_ERR_UNSUPPORTED = 3 /* combination not compiled into this library */
 };
 
-/* Elements handled by one lane per tile; a tile is block_size * this many
- * elements and is processed by one workgroup.  Hosts use it to lay out the
- * tile ranges of sr_row tables. */
-#define SR_ELEMENTS_PER_THREAD 4
+/* Elements one lane moves per tile.  A tile is block_size * (this many)
+ * consecutive elements of one tensor and is processed by one workgroup.
+ * Launches that store a one-byte format (E4M3, E5M2) use the narrow width,
+ * so that each lane moves at least 8 bytes of every operand; all others
+ * move FP32 operands as one 128-bit access per lane.  sr_lane_elements()
+ * returns the width of a given launch. */
+#define SR_LANE_ELEMENTS 4
+#define SR_LANE_ELEMENTS_NARROW 8
 
 /* Row flag: every pointer of the row is 16-byte aligned, so full tiles take
  * the 128-bit vector path.  Rows without it take the coalesced scalar path. */
@@ -109,6 +113,15 @@ int sr_abi_version(void);
 
 /* Message of the last failure on this thread ("" if none). */
 const char* sr_last_error(void);
+
+/* Elements per lane (SR_LANE_ELEMENTS or SR_LANE_ELEMENTS_NARROW) of a
+ * launch whose stored formats are state0_dtype and state1_dtype: the two
+ * AdamW moments, the SGDM momentum given twice, or a cast's output given
+ * twice.  Hosts lay out the tile ranges of sr_row tables with tiles of
+ * block_size * sr_lane_elements(...) elements.  Returns 0 for an unknown
+ * dtype.  No reference counterpart: the reference's Triton launches take
+ * BLOCK_SIZE elements per program (sr_states/triton/_common.py:47-60). */
+int sr_lane_elements(int state0_dtype, int state1_dtype);
 
 /* ---- counter-hash keys (host) ----------------------------------------- */
 

@@ -87,9 +87,10 @@ int launch(const void* fn, int block, uint32_t tiles, void* arg, void* stream) {
   return SR_OK;
 }
 
-// Tiles covering n elements, or fail if they do not fit 32-bit tile indices.
-int tiles_for(int64_t n, int block, uint32_t* tiles) {
-  const int64_t tile = static_cast<int64_t>(block) * sr::kEpt;
+// Tiles of block * lanes elements covering n elements, or fail if they do
+// not fit 32-bit tile indices.
+int tiles_for(int64_t n, int block, int lanes, uint32_t* tiles) {
+  const int64_t tile = static_cast<int64_t>(block) * lanes;
   const int64_t count = (n + tile - 1) / tile;
   if (count > 0xFFFFFFFFll) return fail(SR_ERR_ARGUMENT, "%lld elements exceed the tile index range", (long long)n);
   *tiles = static_cast<uint32_t>(count);
@@ -110,6 +111,13 @@ extern "C" {
 int sr_abi_version(void) { return SR_ABI_VERSION; }
 
 const char* sr_last_error(void) { return g_error.c_str(); }
+
+int sr_lane_elements(int state0_dtype, int state1_dtype) {
+  // Rounding rules do not change widths; the nearest-rule encodings stand in.
+  const int a = state_enc(state0_dtype, SR_NEAREST), b = state_enc(state1_dtype, SR_NEAREST);
+  if (a < 0 || b < 0) return 0;
+  return sr::lane_elements(a, b);
+}
 
 uint32_t sr_update_key(uint64_t seed, uint64_t step, uint32_t param_index) {
   return sr::update_key(static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32),
@@ -132,7 +140,7 @@ int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule, uint32_t see
   a.n = n;
   a.counter_base = seed + offset;
   a.vector_ok = aligned16(x) && aligned16(y);
-  if (int rc = tiles_for(n, block_size, &a.total_tiles)) return rc;
+  if (int rc = tiles_for(n, block_size, sr::lane_elements(enc, enc), &a.total_tiles)) return rc;
   return launch(tables().cast[enc], block_size, a.total_tiles, &a, stream);
 }
 
@@ -152,7 +160,7 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n, int p_dty
   a.rows = nullptr;
   a.tile_rows = nullptr;
   a.s = adamw_scalars(*hp);
-  if (int rc = tiles_for(n, block_size, &a.total_tiles)) return rc;
+  if (int rc = tiles_for(n, block_size, sr::lane_elements(me, ve), &a.total_tiles)) return rc;
   sr_row& r = a.inline_row;
   r.ptr[0] = reinterpret_cast<uint64_t>(p);
   r.ptr[1] = reinterpret_cast<uint64_t>(g);
@@ -208,7 +216,7 @@ int sr_sgdm_step(void* p, const void* g, void* u, int64_t n, int p_dtype, int g_
   a.rows = nullptr;
   a.tile_rows = nullptr;
   a.s = {hp->momentum, hp->neg_lr};
-  if (int rc = tiles_for(n, block_size, &a.total_tiles)) return rc;
+  if (int rc = tiles_for(n, block_size, sr::lane_elements(ue, ue), &a.total_tiles)) return rc;
   sr_row& r = a.inline_row;
   r.ptr[0] = reinterpret_cast<uint64_t>(p);
   r.ptr[1] = reinterpret_cast<uint64_t>(g);

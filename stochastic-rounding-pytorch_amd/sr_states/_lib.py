@@ -10,14 +10,17 @@ from __future__ import annotations
 
 import ctypes
 import threading
+from functools import cache
 from pathlib import Path
 
 import numpy as np
 import torch  # noqa: F401  (load torch's HIP runtime before the library)
 
 LIBRARY_PATH = Path(__file__).with_name("libsr_states_hip.so")
-ABI_VERSION = 2
-ELEMENTS_PER_THREAD = 4
+ABI_VERSION = 3
+# Elements per lane of a launch (SR_LANE_ELEMENTS / _NARROW); lane_elements()
+# gives the width of a particular launch.
+LANE_ELEMENTS, LANE_ELEMENTS_NARROW = 4, 8
 
 # enum sr_dtype / sr_rule
 SR_F32, SR_BF16, SR_F16, SR_E4M3, SR_E5M2 = range(5)
@@ -79,6 +82,7 @@ _vp, _i64, _u32, _u64, _int = (
 SIGNATURES = {
     "sr_abi_version": (_int, []),
     "sr_last_error": (ctypes.c_char_p, []),
+    "sr_lane_elements": (_int, [_int, _int]),
     "sr_update_key": (_u32, [_u64, _u64, _u32]),
     "sr_state_key": (_u32, [_u32, _u32]),
     "sr_cast": (_int, [_vp, _vp, _i64, _int, _int, _u32, _u32, _int, _vp]),
@@ -141,6 +145,15 @@ def check(name: str, status: int) -> None:
 def call(name: str, *args) -> None:
     """Call a status-returning entry point and raise RuntimeError on failure."""
     check(name, getattr(library(), name)(*args))
+
+
+@cache
+def lane_elements(state0: torch.dtype, state1: torch.dtype) -> int:
+    """Elements per lane of a launch storing these two dtypes (one state: pass it twice)."""
+    lanes = library().sr_lane_elements(DTYPE_CODES[state0], DTYPE_CODES[state1])
+    if lanes <= 0:
+        raise ValueError(f"no lane width for state dtypes {state0} and {state1}")
+    return lanes
 
 
 def stream_handle(device: torch.device) -> int:

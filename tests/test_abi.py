@@ -27,6 +27,7 @@ def test_header_declares_the_expected_surface():
         [
             "sr_abi_version",
             "sr_last_error",
+            "sr_lane_elements",
             "sr_update_key",
             "sr_state_key",
             "sr_cast",
@@ -53,7 +54,8 @@ def test_header_constants_match_the_binding():
 
     text = HEADER.read_text()
     assert f"#define SR_ABI_VERSION {_lib.ABI_VERSION}" in text
-    assert f"#define SR_ELEMENTS_PER_THREAD {_lib.ELEMENTS_PER_THREAD}" in text
+    assert f"#define SR_LANE_ELEMENTS {_lib.LANE_ELEMENTS}" in text
+    assert f"#define SR_LANE_ELEMENTS_NARROW {_lib.LANE_ELEMENTS_NARROW}" in text
     assert "#define SR_ROW_VECTOR 1u" in text and _lib.ROW_VECTOR == 1
     assert "#define SR_ROW_KEYED 2u" in text and _lib.ROW_KEYED == 2
     assert _lib.ROW_DTYPE.itemsize == 64
@@ -84,3 +86,20 @@ def test_call_raises_with_the_library_message():
 
     with pytest.raises(RuntimeError, match="unsupported cast dtype"):
         _lib.call("sr_cast", None, None, 16, 9, 0, 0, 0, 256, None)
+
+
+def test_lane_width_follows_the_narrowest_stored_format():
+    """8 elements per lane exactly when a stored format is one byte wide; 0 for unknown dtypes."""
+    import torch
+
+    from sr_states import _lib
+
+    lib = _lib.library()
+    widths = {_lib.SR_F32: 4, _lib.SR_BF16: 2, _lib.SR_F16: 2, _lib.SR_E4M3: 1, _lib.SR_E5M2: 1}
+    for a, wa in widths.items():
+        for b, wb in widths.items():
+            expected = _lib.LANE_ELEMENTS_NARROW if min(wa, wb) == 1 else _lib.LANE_ELEMENTS
+            assert lib.sr_lane_elements(a, b) == expected, (a, b)
+    assert lib.sr_lane_elements(5, 0) == 0 and lib.sr_lane_elements(0, -1) == 0
+    assert _lib.lane_elements(torch.float8_e4m3fn, torch.bfloat16) == 8
+    assert _lib.lane_elements(torch.bfloat16, torch.bfloat16) == 4

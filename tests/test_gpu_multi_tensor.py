@@ -58,7 +58,7 @@ def test_multi_tensor_matches_functional_updates_byte_for_byte(cuda, kind, dtype
     cls = sr_states.AdamWHip if adamw else sr_states.SGDMHip
     update = sr_states.hip_adamw_step_ if adamw else sr_states.hip_sgdm_step_
     block_size = 128
-    chunk = block_size * sr_states._lib.ELEMENTS_PER_THREAD
+    chunk = block_size * sr_states._lib.lane_elements(dtype, dtype)
     start_step = 2**32 + 8
 
     class OffsetOptimizer(cls):
@@ -212,7 +212,7 @@ def test_one_launch_per_bucket_and_no_launch_on_validation_error(cuda, kind, mon
         return launch(tables, *args)
 
     monkeypatch.setattr(module, "_launch", count)
-    tile = 256 * sr_states._lib.ELEMENTS_PER_THREAD
+    tile = 256 * sr_states._lib.LANE_ELEMENTS  # BF16 moments
 
     def parameter(n, dtype=torch.float32):
         p = torch.nn.Parameter(torch.ones(n, device=cuda, dtype=dtype))

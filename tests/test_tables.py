@@ -57,10 +57,10 @@ def test_buckets_split_device_dtypes_and_adamw_steps():
 
 
 def test_records_and_tile_map_layout():
-    tile = 128 * _lib.ELEMENTS_PER_THREAD
+    tile = 128 * _lib.LANE_ELEMENTS
     layout = [(1, 3, 2**32 - 20), (tile - 1, 4, 5), (tile, 2**32 + 6, 0), (tile + 1, 7, 2**33 + 1)]
     pointers = [(16 * k, 16 * k + 32, 64, 80 + (k == 2) * 4) for k in range(4)]
-    records = build_records(layout, pointers, 128)
+    records = build_records(layout, pointers, tile)
     assert records["numel"].tolist() == [1, tile - 1, tile, tile + 1]
     assert records["tile_begin"].tolist() == [0, 1, 2, 3]
     assert records["tile_end"].tolist() == [1, 2, 3, 5]
@@ -68,19 +68,20 @@ def test_records_and_tile_map_layout():
     assert records["shard_start"].tolist() == [2**32 - 20, 5, 0, 1]
     assert records["flags"].tolist() == [_lib.ROW_VECTOR, _lib.ROW_VECTOR, 0, _lib.ROW_VECTOR]
     assert records["ptr"][2].tolist() == [32, 64, 64, 84]
-    assert build_tile_rows(layout, 128).tolist() == [0, 1, 2, 3, 3]
+    assert build_tile_rows(layout, tile).tolist() == [0, 1, 2, 3, 3]
     # SGDM rows carry three pointers; the fourth is zero.
-    assert build_records([(5, 0, 0)], [(16, 32, 48)], 256)["ptr"][0].tolist() == [16, 32, 48, 0]
+    assert build_records([(5, 0, 0)], [(16, 32, 48)], 1024)["ptr"][0].tolist() == [16, 32, 48, 0]
 
 
 @pytest.mark.parametrize("block", [128, 256, 1024])
-def test_tile_map_covers_every_element_once(block):
+@pytest.mark.parametrize("lanes", [_lib.LANE_ELEMENTS, _lib.LANE_ELEMENTS_NARROW])
+def test_tile_map_covers_every_element_once(block, lanes):
     """Property: each tile belongs to exactly one row and covers its elements in order."""
     gen = np.random.default_rng(5)
     layout = [(int(n), i, 0) for i, n in enumerate(gen.integers(1, 50_000, size=200))]
-    tile = block * _lib.ELEMENTS_PER_THREAD
-    records = build_records(layout, [(0, 0, 0)] * len(layout), block)
-    tile_rows = build_tile_rows(layout, block)
+    tile = block * lanes
+    records = build_records(layout, [(0, 0, 0)] * len(layout), tile)
+    tile_rows = build_tile_rows(layout, tile)
     assert len(tile_rows) == records["tile_end"][-1]
     for r, rec in enumerate(records):
         owned = np.nonzero(tile_rows == r)[0]
@@ -225,7 +226,7 @@ def test_launch_scalars_are_the_eager_fp32_roundings(recorder):
 
 def test_one_table_per_bucket_and_no_launch_on_validation_error(recorder):
     """tests/test_triton_multi_tensor.py:184-228 on CPU."""
-    tile = 256 * _lib.ELEMENTS_PER_THREAD
+    tile = 256 * _lib.LANE_ELEMENTS  # BF16 moments
 
     def parameter(n, dtype=torch.float32):
         p = torch.nn.Parameter(torch.ones(n, dtype=dtype))
@@ -312,3 +313,18 @@ def test_library_is_the_only_execution_path(monkeypatch):
     monkeypatch.setattr(_lib, "LIBRARY_PATH", _lib.LIBRARY_PATH.with_name("missing.so"))
     with pytest.raises(RuntimeError, match="not built"):
         sr_states.update_key(1, 2, 3)
+
+
+def test_fp8_buckets_use_narrow_lane_tiles(recorder):
+    """A bucket storing a one-byte state is tiled at 8 elements per lane, others at 4."""
+    n, block = 5000, 256
+    params = [torch.nn.Parameter(torch.ones(n)) for _ in range(2)]
+    fp8 = {"exp_avg": StateFormat(torch.float8_e4m3fn), "exp_avg_sq": StateFormat(torch.bfloat16)}
+    for p in params:
+        p.grad = torch.ones(n)
+    AdamWHip([params[0]], lr=0.01, state_format=fp8, block_size=block).step()
+    AdamWHip([params[1]], lr=0.01, block_size=block).step()
+    narrow, wide = (launch["tables"] for launch in recorder)
+    assert narrow.total_tiles == -(-n // (block * _lib.LANE_ELEMENTS_NARROW)) == 3
+    assert wide.total_tiles == -(-n // (block * _lib.LANE_ELEMENTS)) == 5
+    assert narrow.records["tile_end"].tolist() == [3] and wide.records["tile_end"].tolist() == [5]
