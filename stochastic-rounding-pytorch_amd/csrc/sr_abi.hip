@@ -72,6 +72,9 @@ int state_enc(int dtype, int rule) {
 // Parameter / gradient storage -> table index (FP32 0, BF16 1), or -1.
 int pg_index(int dtype) { return dtype == SR_F32 ? 0 : (dtype == SR_BF16 ? 1 : -1); }
 
+// Encoding of a parameter or gradient table index (FP32, or BF16 nearest).
+int param_enc(int index) { return index == 0 ? sr::ENC_F32 : sr::ENC_BF16_RN; }
+
 bool valid_block(int block) { return block >= 64 && block <= sr::kMaxBlock && block % 64 == 0; }
 
 // One workgroup per tile; the grid is padded to a whole number of XCD chunk
@@ -112,11 +115,12 @@ int sr_abi_version(void) { return SR_ABI_VERSION; }
 
 const char* sr_last_error(void) { return g_error.c_str(); }
 
-int sr_lane_elements(int state0_dtype, int state1_dtype) {
+int sr_lane_elements(int p_dtype, int g_dtype, int state0_dtype, int state1_dtype) {
   // Rounding rules do not change widths; the nearest-rule encodings stand in.
+  const int p = state_enc(p_dtype, SR_NEAREST), g = state_enc(g_dtype, SR_NEAREST);
   const int a = state_enc(state0_dtype, SR_NEAREST), b = state_enc(state1_dtype, SR_NEAREST);
-  if (a < 0 || b < 0) return 0;
-  return sr::lane_elements(a, b);
+  if (p < 0 || g < 0 || a < 0 || b < 0) return 0;
+  return sr::lane_elements(p, g, a, b);
 }
 
 uint32_t sr_update_key(uint64_t seed, uint64_t step, uint32_t param_index) {
@@ -140,7 +144,8 @@ int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule, uint32_t see
   a.n = n;
   a.counter_base = seed + offset;
   a.vector_ok = aligned16(x) && aligned16(y);
-  if (int rc = tiles_for(n, block_size, sr::lane_elements(enc, enc), &a.total_tiles)) return rc;
+  const int lanes = sr::lane_elements(sr::ENC_F32, sr::ENC_F32, enc, enc);
+  if (int rc = tiles_for(n, block_size, lanes, &a.total_tiles)) return rc;
   return launch(tables().cast[enc], block_size, a.total_tiles, &a, stream);
 }
 
@@ -160,7 +165,8 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n, int p_dty
   a.rows = nullptr;
   a.tile_rows = nullptr;
   a.s = adamw_scalars(*hp);
-  if (int rc = tiles_for(n, block_size, sr::lane_elements(me, ve), &a.total_tiles)) return rc;
+  const int lanes = sr::lane_elements(param_enc(pi), param_enc(gi), me, ve);
+  if (int rc = tiles_for(n, block_size, lanes, &a.total_tiles)) return rc;
   sr_row& r = a.inline_row;
   r.ptr[0] = reinterpret_cast<uint64_t>(p);
   r.ptr[1] = reinterpret_cast<uint64_t>(g);
@@ -216,7 +222,8 @@ int sr_sgdm_step(void* p, const void* g, void* u, int64_t n, int p_dtype, int g_
   a.rows = nullptr;
   a.tile_rows = nullptr;
   a.s = {hp->momentum, hp->neg_lr};
-  if (int rc = tiles_for(n, block_size, sr::lane_elements(ue, ue), &a.total_tiles)) return rc;
+  const int lanes = sr::lane_elements(param_enc(pi), param_enc(gi), ue, ue);
+  if (int rc = tiles_for(n, block_size, lanes, &a.total_tiles)) return rc;
   sr_row& r = a.inline_row;
   r.ptr[0] = reinterpret_cast<uint64_t>(p);
   r.ptr[1] = reinterpret_cast<uint64_t>(g);

@@ -3,11 +3,13 @@
 // Work decomposition.  Every launch covers a range of tiles; a tile is
 // blockDim.x * E consecutive elements of one tensor and is processed by
 // exactly one workgroup (no persistent loop).  A lane owns E consecutive
-// elements: E = 4 moves FP32 operands as one 128-bit access per lane and
-// 16-bit states as one 64-bit access; launches that store a one-byte format
-// use E = 8, so FP8 states move as 64-bit accesses rather than 32-bit ones
-// (measured: 5.50 vs 5.27 TB/s for E4M3 + BF16 moments, while BF16-only
-// launches are faster at E = 4).  Rows whose pointers are not all 16-byte
+// elements.  E = 4 when the widest operand is FP32 and none is narrower than
+// 16 bits: FP32 operands move as one 128-bit access per lane, 16-bit states
+// as one 64-bit access.  Every other launch uses E = 8, so that no lane
+// access is narrower than 64 bits.  Measured on MI355X: E4M3 + BF16 moments
+// 5.27 -> 5.50 TB/s at E = 8; BF16 parameters and moments 4.61 -> 4.99 TB/s;
+// BF16 SGDM 4.96 -> 5.76 TB/s; FP32 parameters with 16-bit states are
+// faster at E = 4 (5.67 vs 5.40 TB/s).  Rows whose pointers are not all 16-byte
 // aligned, and the partial last tile of a row, take a coalesced scalar path
 // (element k*blockDim.x + lane of the tile).
 //
@@ -32,11 +34,16 @@
 
 namespace sr {
 
-// Elements per lane of a launch storing encodings a and b (the host's
-// sr_lane_elements() applies the same rule to dtypes).
-constexpr int lane_elements(int enc_a, int enc_b) {
-  return (enc_bytes(enc_a) == 1 || enc_bytes(enc_b) == 1) ? SR_LANE_ELEMENTS_NARROW
-                                                          : SR_LANE_ELEMENTS;
+// Elements per lane of a launch whose operands have encodings p, g, a, b
+// (the host's sr_lane_elements() applies the same rule to dtypes).
+constexpr int lane_elements(int p, int g, int a, int b) {
+  const int w[4] = {enc_bytes(p), enc_bytes(g), enc_bytes(a), enc_bytes(b)};
+  int lo = w[0], hi = w[0];
+  for (int k = 1; k < 4; ++k) {
+    lo = w[k] < lo ? w[k] : lo;
+    hi = w[k] > hi ? w[k] : hi;
+  }
+  return (hi == 4 && lo >= 2) ? SR_LANE_ELEMENTS : SR_LANE_ELEMENTS_NARROW;
 }
 static_assert(SR_LANE_ELEMENTS == 4 && SR_LANE_ELEMENTS_NARROW == 8, "lanes move 4 or 8 elements");
 constexpr int kMaxBlock = 1024;
@@ -186,7 +193,7 @@ __device__ __forceinline__ uint32_t row_key(const Args& a, const sr_row& r) {
 template <int PE, int GE, int ME, int VE>
 __device__ __forceinline__ void adamw_vector(char* p, const char* g, char* m, char* v, int64_t i,
                                              uint32_t cm, uint32_t cv, const AdamWScalars& s) {
-  constexpr int E = lane_elements(ME, VE);
+  constexpr int E = lane_elements(PE, GE, ME, VE);
   uint32_t rp[E], rg[E], rm[E], rv[E];
   load_vec<PE>(p, i, rp);
   load_vec<GE>(g, i, rg);
@@ -221,7 +228,7 @@ __device__ __forceinline__ void adamw_scalar(char* p, const char* g, char* m, ch
 
 template <int PE, int GE, int ME, int VE>
 __global__ __launch_bounds__(kMaxBlock) void adamw_kernel(const AdamWArgs a) {
-  constexpr int E = lane_elements(ME, VE);
+  constexpr int E = lane_elements(PE, GE, ME, VE);
   const uint32_t t = logical_tile(a.total_tiles);
   if (t >= a.total_tiles) return;
   const sr_row& r = tile_row(a, t);
@@ -253,7 +260,7 @@ __global__ __launch_bounds__(kMaxBlock) void adamw_kernel(const AdamWArgs a) {
 template <int PE, int GE, int UE>
 __device__ __forceinline__ void sgdm_vector(char* p, const char* g, char* u, int64_t i, uint32_t cu,
                                             const SgdmScalars& s) {
-  constexpr int E = lane_elements(UE, UE);
+  constexpr int E = lane_elements(PE, GE, UE, UE);
   uint32_t rp[E], rg[E], ru[E];
   load_vec<PE>(p, i, rp);
   load_vec<GE>(g, i, rg);
@@ -282,7 +289,7 @@ __device__ __forceinline__ void sgdm_scalar(char* p, const char* g, char* u, int
 
 template <int PE, int GE, int UE>
 __global__ __launch_bounds__(kMaxBlock) void sgdm_kernel(const SgdmArgs a) {
-  constexpr int E = lane_elements(UE, UE);
+  constexpr int E = lane_elements(PE, GE, UE, UE);
   const uint32_t t = logical_tile(a.total_tiles);
   if (t >= a.total_tiles) return;
   const sr_row& r = tile_row(a, t);
@@ -309,7 +316,7 @@ __global__ __launch_bounds__(kMaxBlock) void sgdm_kernel(const SgdmArgs a) {
 // ---------------------------------------------------------------------------
 template <int ENC>
 __global__ __launch_bounds__(kMaxBlock) void cast_kernel(const CastArgs a) {
-  constexpr int E = lane_elements(ENC, ENC);
+  constexpr int E = lane_elements(ENC_F32, ENC_F32, ENC, ENC);
   const uint32_t t = logical_tile(a.total_tiles);
   if (t >= a.total_tiles) return;
   const uint32_t tile = blockDim.x * E;

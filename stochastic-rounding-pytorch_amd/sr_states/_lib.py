@@ -82,7 +82,7 @@ _vp, _i64, _u32, _u64, _int = (
 SIGNATURES = {
     "sr_abi_version": (_int, []),
     "sr_last_error": (ctypes.c_char_p, []),
-    "sr_lane_elements": (_int, [_int, _int]),
+    "sr_lane_elements": (_int, [_int, _int, _int, _int]),
     "sr_update_key": (_u32, [_u64, _u64, _u32]),
     "sr_state_key": (_u32, [_u32, _u32]),
     "sr_cast": (_int, [_vp, _vp, _i64, _int, _int, _u32, _u32, _int, _vp]),
@@ -148,11 +148,14 @@ def call(name: str, *args) -> None:
 
 
 @cache
-def lane_elements(state0: torch.dtype, state1: torch.dtype) -> int:
-    """Elements per lane of a launch storing these two dtypes (one state: pass it twice)."""
-    lanes = library().sr_lane_elements(DTYPE_CODES[state0], DTYPE_CODES[state1])
+def lane_elements(*dtypes: torch.dtype) -> int:
+    """Elements per lane of a launch with (parameter, gradient, state0, state1) dtypes.
+
+    SGDM passes its momentum dtype twice.
+    """
+    lanes = library().sr_lane_elements(*(DTYPE_CODES[d] for d in dtypes))
     if lanes <= 0:
-        raise ValueError(f"no lane width for state dtypes {state0} and {state1}")
+        raise ValueError(f"no lane width for operand dtypes {dtypes}")
     return lanes
 
 

@@ -58,7 +58,8 @@ def test_multi_tensor_matches_functional_updates_byte_for_byte(cuda, kind, dtype
     cls = sr_states.AdamWHip if adamw else sr_states.SGDMHip
     update = sr_states.hip_adamw_step_ if adamw else sr_states.hip_sgdm_step_
     block_size = 128
-    chunk = block_size * sr_states._lib.lane_elements(dtype, dtype)
+    # The widest tile among the test's buckets (8 lanes for FP8 states).
+    chunk = block_size * sr_states._lib.lane_elements(torch.float32, torch.float32, dtype, dtype)
     start_step = 2**32 + 8
 
     class OffsetOptimizer(cls):

@@ -315,16 +315,17 @@ def test_library_is_the_only_execution_path(monkeypatch):
         sr_states.update_key(1, 2, 3)
 
 
-def test_fp8_buckets_use_narrow_lane_tiles(recorder):
-    """A bucket storing a one-byte state is tiled at 8 elements per lane, others at 4."""
+def test_buckets_are_tiled_at_their_lane_width(recorder):
+    """FP8 states or all-16-bit operands: 8 elements per lane; FP32 with 16-bit states: 4."""
     n, block = 5000, 256
-    params = [torch.nn.Parameter(torch.ones(n)) for _ in range(2)]
     fp8 = {"exp_avg": StateFormat(torch.float8_e4m3fn), "exp_avg_sq": StateFormat(torch.bfloat16)}
-    for p in params:
-        p.grad = torch.ones(n)
-    AdamWHip([params[0]], lr=0.01, state_format=fp8, block_size=block).step()
-    AdamWHip([params[1]], lr=0.01, block_size=block).step()
-    narrow, wide = (launch["tables"] for launch in recorder)
-    assert narrow.total_tiles == -(-n // (block * _lib.LANE_ELEMENTS_NARROW)) == 3
-    assert wide.total_tiles == -(-n // (block * _lib.LANE_ELEMENTS)) == 5
-    assert narrow.records["tile_end"].tolist() == [3] and wide.records["tile_end"].tolist() == [5]
+    cases = [(torch.float32, fp8, _lib.LANE_ELEMENTS_NARROW), (torch.bfloat16, None, _lib.LANE_ELEMENTS_NARROW),
+             (torch.float32, None, _lib.LANE_ELEMENTS)]
+    for dtype, formats, _ in cases:
+        p = torch.nn.Parameter(torch.ones(n, dtype=dtype))
+        p.grad = torch.ones_like(p)
+        AdamWHip([p], lr=0.01, state_format=formats, block_size=block).step()
+    for launch, (_, _, lanes) in zip(recorder, cases):
+        tiles = -(-n // (block * lanes))
+        assert launch["tables"].total_tiles == tiles
+        assert launch["tables"].records["tile_end"].tolist() == [tiles]
