@@ -158,6 +158,10 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n,
 /* One bucket: `rows` is a device table of nrows sr_row records whose tile
  * ranges cover [0, total_tiles) in order, and `tile_rows` a device array of
  * total_tiles row indices (tile_rows[t] = the row whose range holds t).
+ * Row r spans ceil(numel / T) tiles of T = block_size *
+ * sr_lane_elements(p_dtype, g_dtype, m_dtype, v_dtype) elements.  The
+ * tables live in device memory and are not checked: tables that break these
+ * rules make the kernel access memory out of bounds.
  * Keys are derived on the device from (seed, rng_step, param_index).
  * Replaces `_multi_adamw_kernel` and its launch
  * (sr_states/triton/adamw.py:102-157, 289-319). */
@@ -174,7 +178,8 @@ int sr_sgdm_step(void* p, const void* g, void* u, int64_t n,
                  const sr_sgdm_hparams* hp, uint32_t key, uint32_t offset,
                  int block_size, void* stream);
 
-/* Same table layout as sr_adamw_multi (state 1 pointer unused).
+/* Same table layout as sr_adamw_multi (state 1 pointer unused); tiles are
+ * block_size * sr_lane_elements(p_dtype, g_dtype, u_dtype, u_dtype) elements.
  * Replaces `_multi_sgdm_kernel` and its launch
  * (sr_states/triton/sgd.py:393-431, 533-556). */
 int sr_sgdm_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint32_t total_tiles,
