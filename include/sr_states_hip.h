@@ -56,12 +56,13 @@ enum sr_error {
 
 /* Elements one lane moves per tile.  A tile is block_size * (this many)
  * consecutive elements of one tensor and is processed by one workgroup.
- * A launch whose widest operand is 4 bytes and narrowest is 2 bytes (FP32
- * parameters with 16-bit states) uses SR_LANE_ELEMENTS: FP32 operands move
- * as one 128-bit access per lane.  Every other launch (a one-byte FP8
- * state, or only 16-bit operands) uses SR_LANE_ELEMENTS_NARROW, so that
- * each lane moves at least 8 bytes of every operand.  sr_lane_elements()
- * returns the width of a given launch. */
+ * An optimizer launch whose widest operand is 4 bytes and narrowest is 2
+ * bytes (FP32 parameters with 16-bit states) uses SR_LANE_ELEMENTS: FP32
+ * operands move as one 128-bit access per lane.  Every other optimizer
+ * launch (a one-byte FP8 state, or only 16-bit operands), and every cast,
+ * uses SR_LANE_ELEMENTS_NARROW, so that each lane moves at least 8 bytes of
+ * every operand.  sr_lane_elements() returns the width of an optimizer
+ * launch. */
 #define SR_LANE_ELEMENTS 4
 #define SR_LANE_ELEMENTS_NARROW 8
 
@@ -116,11 +117,12 @@ int sr_abi_version(void);
 /* Message of the last failure on this thread ("" if none). */
 const char* sr_last_error(void);
 
-/* Elements per lane (SR_LANE_ELEMENTS or SR_LANE_ELEMENTS_NARROW) of a
- * launch with these operand dtypes: parameter, gradient and the two AdamW
- * moments; for SGDM the momentum dtype twice; for a cast SR_F32 twice, then
- * the output dtype twice.  Hosts lay out the tile ranges of sr_row tables
- * with tiles of block_size * sr_lane_elements(...) elements.  Returns 0 for
+/* Elements per lane (SR_LANE_ELEMENTS or SR_LANE_ELEMENTS_NARROW) of an
+ * optimizer launch with these operand dtypes: parameter, gradient and the
+ * two AdamW moments, or for SGDM the momentum dtype twice.  Hosts lay out
+ * the tile ranges of sr_row tables with tiles of
+ * block_size * sr_lane_elements(...) elements.  (Casts lay out their own
+ * tiles and always move SR_LANE_ELEMENTS_NARROW elements per lane.)  Returns 0 for
  * an unknown dtype.  No reference counterpart: the reference's Triton
  * launches take BLOCK_SIZE elements per program
  * (sr_states/triton/_common.py:47-60). */

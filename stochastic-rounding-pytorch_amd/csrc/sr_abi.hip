@@ -144,8 +144,7 @@ int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule, uint32_t see
   a.n = n;
   a.counter_base = seed + offset;
   a.vector_ok = aligned16(x) && aligned16(y);
-  const int lanes = sr::lane_elements(sr::ENC_F32, sr::ENC_F32, enc, enc);
-  if (int rc = tiles_for(n, block_size, lanes, &a.total_tiles)) return rc;
+  if (int rc = tiles_for(n, block_size, sr::kCastLaneElements, &a.total_tiles)) return rc;
   return launch(tables().cast[enc], block_size, a.total_tiles, &a, stream);
 }
 
