@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SR_ABI_VERSION 3
+#define SR_ABI_VERSION 4
 
 /* Storage dtypes (torch.float32, bfloat16, float16, float8_e4m3fn,
  * float8_e5m2).  The set mirrors the built-in rounding table of the
@@ -160,6 +160,12 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n,
 /* One bucket: `rows` is a device table of nrows sr_row records whose tile
  * ranges cover [0, total_tiles) in order, and `tile_rows` a device array of
  * total_tiles row indices (tile_rows[t] = the row whose range holds t).
+ * `row_scalars` is NULL when every row has the same AdamW step (hp then
+ * holds its scalars), or a device array of 2 * nrows floats holding each
+ * row's (neg_step_size, correction2_sqrt); the other scalars come from hp.
+ * The reference launches once per distinct step instead
+ * (sr_states/triton/_multi_tensor.py:22-36); the per-row pair keeps one
+ * launch per bucket with the same FP32 scalars per row.
  * Row r spans ceil(numel / T) tiles of T = block_size *
  * sr_lane_elements(p_dtype, g_dtype, m_dtype, v_dtype) elements.  The
  * tables live in device memory and are not checked: tables that break these
@@ -167,7 +173,8 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n,
  * Keys are derived on the device from (seed, rng_step, param_index).
  * Replaces `_multi_adamw_kernel` and its launch
  * (sr_states/triton/adamw.py:102-157, 289-319). */
-int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint32_t total_tiles,
+int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, const float* row_scalars,
+                   int nrows, uint32_t total_tiles,
                    int p_dtype, int g_dtype, int m_dtype, int m_rule,
                    int v_dtype, int v_rule, const sr_adamw_hparams* hp,
                    uint64_t seed, uint64_t rng_step, int block_size, void* stream);

@@ -2,23 +2,26 @@
 // step's host side.
 //
 // The reference validates and buckets every tensor of a group on every step
-// (sr_states/triton/_multi_tensor.py:22-34 and :61-88).  Its row tables only
-// change when a layout, an address, the set of parameters with gradients or
-// the step counter changes, so this module condenses exactly those facts into
-// one byte string per step.  The Python side runs the full validation and
-// rebuilds the tables whenever the string differs from the one recorded at the
-// last fully validated step; when it is equal, nothing the validation or the
-// tables depend on has changed and the recorded launches are reused.
+// (sr_states/triton/_multi_tensor.py:22-34 and :61-88).  The row tables only
+// change when a layout, an address or the set of parameters with gradients
+// changes, so this module condenses exactly those facts into one byte string
+// per step.  The Python side runs the full validation and rebuilds the tables
+// whenever the string differs from the one recorded at the last fully
+// validated step; when it is equal, nothing the validation or the tables
+// depend on has changed and the recorded launches are reused.
 //
 // group_signature(params, state, state_names, uses_step, first_index)
-//     -> (bytes, step, entries) or None
+//     -> (bytes, step, steps, entries) or None
 //   Each tensor contributes its Python type, so a validated step vouches only
 //   for the types it saw.  None means "take the validating path": an object
 //   that is not a tensor, a missing state, a non-strided tensor, one with
-//   elements but no memory (wrapper subclasses), a step that is not an int,
-//   steps that differ between parameters, or no parameter with a gradient.  ``step`` is the common stored
-//   step (0 when absent); it is 0 when uses_step is false.  ``entries`` lists
-//   the state dict of every parameter with a gradient, in group order.
+//   elements but no memory (wrapper subclasses), a stored step that is not a
+//   non-negative int, or no parameter with a gradient.  Stored steps are not
+//   part of the bytes.  When uses_step is true and every parameter with a
+//   gradient stores the same step (0 when absent), ``step`` is that value and
+//   ``steps`` is None; when they differ, ``step`` is None and ``steps`` lists
+//   them in group order.  Both are None when uses_step is false.  ``entries``
+//   lists the state dict of every parameter with a gradient, in group order.
 //
 // set_steps(entries, value)
 //   entry["step"] = value for every dict in the list ``entries``.
@@ -103,13 +106,12 @@ bool walk_parameter(PyObject* parameter, PyObject* gradient, PyObject* state, Py
   if (!PyLong_CheckExact(value)) return false;
   int overflow = 0;
   step = PyLong_AsLongLongAndOverflow(value, &overflow);
-  return !overflow && !PyErr_Occurred();
+  return !overflow && !PyErr_Occurred() && step >= 0;
 }
 
 // The walk proper; returns false for "take the validating path".
 bool walk(PyObject* params, PyObject* state, PyObject* names, bool uses_step,
-          std::vector<int64_t>& words, int64_t& common_step, PyObject* entries) {
-  bool any = false;
+          std::vector<int64_t>& words, std::vector<int64_t>& steps, PyObject* entries) {
   for (Py_ssize_t i = 0; i < PyList_GET_SIZE(params); ++i) {
     PyObject* parameter = PyList_GET_ITEM(params, i);
     Ref hold_parameter(parameter);
@@ -125,11 +127,9 @@ bool walk(PyObject* params, PyObject* state, PyObject* names, bool uses_step,
     if (!walk_parameter(parameter, gradient.obj, state, names, uses_step, words, step, entries)) {
       return false;
     }
-    if (any && step != common_step) return false;
-    common_step = step;
-    any = true;
+    steps.push_back(step);
   }
-  return any;
+  return !steps.empty();
 }
 
 PyObject* group_signature(PyObject*, PyObject* args) {
@@ -144,13 +144,13 @@ PyObject* group_signature(PyObject*, PyObject* args) {
   words.reserve(4 + PyList_GET_SIZE(params) * (1 + 7 * (2 + PyTuple_GET_SIZE(names))));
   words.push_back(first_index);
   words.push_back(PyList_GET_SIZE(params));
-  int64_t step = 0;
+  std::vector<int64_t> steps;
   bool found = false;
   Ref entries(PyList_New(0));
   if (entries.obj == nullptr) return nullptr;
   Py_INCREF(params);  // the walk may run Python code (Tensor.__hash__)
   try {
-    found = walk(params, state, names, uses_step != 0, words, step, entries.obj);
+    found = walk(params, state, names, uses_step != 0, words, steps, entries.obj);
   } catch (...) {
     found = false;
   }
@@ -159,9 +159,28 @@ PyObject* group_signature(PyObject*, PyObject* args) {
     PyErr_Clear();
     Py_RETURN_NONE;
   }
-  return Py_BuildValue("(y#LO)", reinterpret_cast<const char*>(words.data()),
-                       static_cast<Py_ssize_t>(words.size() * sizeof(int64_t)),
-                       static_cast<long long>(uses_step ? step : 0), entries.obj);
+  bool uniform = true;
+  for (int64_t s : steps) uniform = uniform && s == steps[0];
+  Ref common(nullptr), listed(nullptr);
+  if (!uses_step) {
+    common.obj = Py_NewRef(Py_None);
+    listed.obj = Py_NewRef(Py_None);
+  } else if (uniform) {
+    common.obj = PyLong_FromLongLong(steps[0]);
+    listed.obj = Py_NewRef(Py_None);
+  } else {
+    common.obj = Py_NewRef(Py_None);
+    listed.obj = PyList_New(static_cast<Py_ssize_t>(steps.size()));
+    for (size_t k = 0; listed.obj != nullptr && k < steps.size(); ++k) {
+      PyObject* value = PyLong_FromLongLong(steps[k]);
+      if (value == nullptr) return nullptr;
+      PyList_SET_ITEM(listed.obj, static_cast<Py_ssize_t>(k), value);
+    }
+  }
+  if (common.obj == nullptr || listed.obj == nullptr) return nullptr;
+  return Py_BuildValue("(y#OOO)", reinterpret_cast<const char*>(words.data()),
+                       static_cast<Py_ssize_t>(words.size() * sizeof(int64_t)), common.obj,
+                       listed.obj, entries.obj);
 }
 
 PyObject* set_steps(PyObject*, PyObject* args) {

@@ -181,7 +181,8 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n, int p_dty
   return launch(tables().adamw[pi][gi][me][ve], block_size, a.total_tiles, &a, stream);
 }
 
-int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint32_t total_tiles,
+int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, const float* row_scalars,
+                   int nrows, uint32_t total_tiles,
                    int p_dtype, int g_dtype,
                    int m_dtype, int m_rule, int v_dtype, int v_rule, const sr_adamw_hparams* hp,
                    uint64_t seed, uint64_t rng_step, int block_size, void* stream) {
@@ -196,6 +197,7 @@ int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uin
   sr::AdamWArgs a{};
   a.rows = rows;
   a.tile_rows = tile_rows;
+  a.row_scalars = row_scalars;
   a.total_tiles = total_tiles;
   a.s = adamw_scalars(*hp);
   a.seed_lo = static_cast<uint32_t>(seed);

@@ -51,6 +51,9 @@ constexpr int kMaxBlock = 1024;
 struct AdamWArgs {
   const sr_row* rows;        // device table; nullptr selects `inline_row`
   const uint32_t* tile_rows; // row of each tile; nullptr with `inline_row`
+  // Per-row (neg_step_size, correction2_sqrt) pairs when the rows' AdamW
+  // steps differ; nullptr: every row uses s.neg_step_size, s.correction2_sqrt.
+  const float* row_scalars;
   sr_row inline_row;
   AdamWScalars s;
   uint32_t total_tiles;
@@ -176,8 +179,16 @@ __device__ __forceinline__ void store1(void* base, int64_t i, uint32_t v) {
 
 // The row record of this workgroup's tile, read once with uniform loads.
 template <class Args>
-__device__ __forceinline__ const sr_row& tile_row(const Args& a, uint32_t t) {
-  return a.rows ? a.rows[a.tile_rows[t]] : a.inline_row;
+__device__ __forceinline__ uint32_t tile_row_index(const Args& a, uint32_t t) {
+  return a.rows ? a.tile_rows[t] : 0u;
+}
+
+// The row record, copied once: one wide uniform load from the table (or the
+// kernel argument) instead of a load per field behind its own branch.
+template <class Args>
+__device__ __forceinline__ sr_row row_record(const Args& a, uint32_t row) {
+  if (a.rows) return a.rows[row];
+  return a.inline_row;
 }
 
 template <class Args>
@@ -231,7 +242,13 @@ __global__ __launch_bounds__(kMaxBlock) void adamw_kernel(const AdamWArgs a) {
   constexpr int E = lane_elements(PE, GE, ME, VE);
   const uint32_t t = logical_tile(a.total_tiles);
   if (t >= a.total_tiles) return;
-  const sr_row& r = tile_row(a, t);
+  const uint32_t row = tile_row_index(a, t);
+  const sr_row r = row_record(a, row);
+  AdamWScalars s = a.s;
+  if (a.row_scalars) {
+    s.neg_step_size = a.row_scalars[2 * row];
+    s.correction2_sqrt = a.row_scalars[2 * row + 1];
+  }
   char* p = reinterpret_cast<char*>(r.ptr[0]);
   const char* g = reinterpret_cast<const char*>(r.ptr[1]);
   char* m = reinterpret_cast<char*>(r.ptr[2]);
@@ -244,12 +261,12 @@ __global__ __launch_bounds__(kMaxBlock) void adamw_kernel(const AdamWArgs a) {
   const int64_t start = static_cast<int64_t>(t - r.tile_begin) * tile;
   if ((r.flags & SR_ROW_VECTOR) && start + tile <= numel) {
     adamw_vector<PE, GE, ME, VE>(p, g, m, v, start + static_cast<int64_t>(threadIdx.x) * E, cm,
-                                 cv, a.s);
+                                 cv, s);
   } else {
 #pragma unroll
     for (int k = 0; k < E; ++k) {
       const int64_t i = start + static_cast<int64_t>(k) * blockDim.x + threadIdx.x;
-      if (i < numel) adamw_scalar<PE, GE, ME, VE>(p, g, m, v, i, cm, cv, a.s);
+      if (i < numel) adamw_scalar<PE, GE, ME, VE>(p, g, m, v, i, cm, cv, s);
     }
   }
 }
@@ -292,7 +309,7 @@ __global__ __launch_bounds__(kMaxBlock) void sgdm_kernel(const SgdmArgs a) {
   constexpr int E = lane_elements(PE, GE, UE, UE);
   const uint32_t t = logical_tile(a.total_tiles);
   if (t >= a.total_tiles) return;
-  const sr_row& r = tile_row(a, t);
+  const sr_row r = row_record(a, tile_row_index(a, t));
   char* p = reinterpret_cast<char*>(r.ptr[0]);
   const char* g = reinterpret_cast<const char*>(r.ptr[1]);
   char* u = reinterpret_cast<char*>(r.ptr[2]);

@@ -17,7 +17,7 @@ import numpy as np
 import torch  # noqa: F401  (load torch's HIP runtime before the library)
 
 LIBRARY_PATH = Path(__file__).with_name("libsr_states_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 # Elements per lane of a launch (SR_LANE_ELEMENTS / _NARROW); lane_elements()
 # gives the width of a particular launch.
 LANE_ELEMENTS, LANE_ELEMENTS_NARROW = 4, 8
@@ -93,7 +93,7 @@ SIGNATURES = {
     ),
     "sr_adamw_multi": (
         _int,
-        [_vp, _vp, _int, _u32, _int, _int, _int, _int, _int, _int,
+        [_vp, _vp, _vp, _int, _u32, _int, _int, _int, _int, _int, _int,
          ctypes.POINTER(AdamWHparams), _u64, _u64, _int, _vp],
     ),
     "sr_sgdm_step": (

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import torch
 
 from .. import _lib
@@ -17,16 +18,21 @@ from ..optim._state import StateOptimizer
 from ..optim.adamw import adamw_hparams, validate_adamw
 from ..rounding import native_codes
 from ._common import validate_device, validate_update_device
-from ._multi_tensor import prepare_group
+from ._multi_tensor import prepare_group, upload
 from ._optimizer import nonnegative, validate_options, validate_tensors
 
 
-def _launch(tables, dtypes, hparams, seed, rng_step, block_size, stream):
-    """One sr_adamw_multi call; dtypes = (p, g, m, m_rule, v, v_rule) codes."""
+def _launch(tables, dtypes, hparams, seed, rng_step, block_size, stream, row_scalars=None):
+    """One sr_adamw_multi call; dtypes = (p, g, m, m_rule, v, v_rule) codes.
+
+    ``row_scalars`` is None when every row shares ``hparams``, else a device
+    tensor of per-row (neg_step_size, correction2_sqrt) FP32 pairs.
+    """
     _lib.call(
         "sr_adamw_multi",
         tables.device_records.data_ptr(),
         tables.device_tile_rows.data_ptr(),
+        None if row_scalars is None else row_scalars.data_ptr(),
         tables.nrows,
         tables.total_tiles,
         *dtypes,
@@ -188,15 +194,27 @@ class AdamWHip(StateOptimizer):
         (m_code, m_rule), (v_code, v_rule) = (native_codes(f.dtype, f.rounding) for f in formats)
         seed, rng_word = _lib.low64(group["sr_seed"]), _lib.low64(rng_step)
         block_size = self._group_block_size(group)
-        for device, step, codes, tables in launches:
-            hparams = adamw_hparams(
+
+        def hparams(step):
+            return adamw_hparams(
                 group["lr"], beta1, beta2, group["eps"], group["weight_decay"], step
             )
-            dtypes = (*codes, m_code, m_rule, v_code, v_rule)
-            with torch.cuda.device(device):
-                _launch(
-                    tables, dtypes, hparams, seed, rng_word, block_size, _lib.stream_handle(device)
-                )
+
+        for launch in launches:
+            dtypes = (*launch.codes, m_code, m_rule, v_code, v_rule)
+            with torch.cuda.device(launch.device):
+                if isinstance(launch.steps, int):
+                    scalars, row_scalars = hparams(launch.steps), None
+                else:
+                    # Rows at different steps: each row's bias-correction pair.
+                    per_step = {step: hparams(step) for step in set(launch.steps)}
+                    pairs = np.array(
+                        [(per_step[s].neg_step_size, per_step[s].correction2_sqrt) for s in launch.steps],
+                        dtype=np.float32,
+                    )
+                    scalars, row_scalars = per_step[launch.steps[0]], upload(pairs, launch.device)
+                stream = _lib.stream_handle(launch.device)
+                _launch(launch.tables, dtypes, scalars, seed, rng_word, block_size, stream, row_scalars)
         record_steps()
 
 

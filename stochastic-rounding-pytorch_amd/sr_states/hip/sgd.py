@@ -155,16 +155,16 @@ class SGDMHip(StateOptimizer):
         hparams = sgdm_hparams(group["lr"], group["momentum"])
         seed, rng_word = _lib.low64(group["sr_seed"]), _lib.low64(rng_step)
         block_size = self._group_block_size(group)
-        for device, _, codes, tables in launches:
-            with torch.cuda.device(device):
+        for launch in launches:
+            with torch.cuda.device(launch.device):
                 _launch(
-                    tables,
-                    (*codes, code, rule),
+                    launch.tables,
+                    (*launch.codes, code, rule),
                     hparams,
                     seed,
                     rng_word,
                     block_size,
-                    _lib.stream_handle(device),
+                    _lib.stream_handle(launch.device),
                 )
         record_steps()
 

@@ -74,7 +74,7 @@ def test_invalid_arguments_fail_before_any_device_work():
     hp = _lib.AdamWHparams()
     assert lib.sr_adamw_step(None, None, None, None, 8, 2, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, 256, None) == 1
     assert b"FP32 or BF16" in lib.sr_last_error()
-    assert lib.sr_adamw_multi(None, None, 1, 1, 0, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, 256, None) == 1
+    assert lib.sr_adamw_multi(None, None, None, 1, 1, 0, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, 256, None) == 1
     assert b"null argument" in lib.sr_last_error()
     sp = _lib.SgdmHparams()
     assert lib.sr_sgdm_multi(None, None, 0, 1, 0, 0, 7, 1, ctypes.byref(sp), 0, 0, 256, None) == 1

@@ -231,7 +231,9 @@ def test_one_launch_per_bucket_and_no_launch_on_validation_error(cuda, kind, mon
     q.grad = torch.ones_like(q)
     tiles.clear()
     opt.step()
-    assert tiles == ([1, 2, 1, 1] if kind == "adamw" else [3, 1, 1])
+    # q's AdamW step now lags p's; the reference would launch the two steps
+    # separately, here they share one launch with per-row bias corrections.
+    assert tiles == [3, 1, 1]
 
     before = p.detach().clone()
     tiles.clear()
@@ -316,3 +318,46 @@ def test_fp32_states_match_torch_optim(cuda, kind):
         torch.testing.assert_close(p, q, rtol=1e-5, atol=1e-6)
         for name in opt._state_names:
             torch.testing.assert_close(opt.state[p][name], native.state[q][name], rtol=1e-5, atol=1e-6)
+
+
+def test_rows_at_different_steps_share_one_launch(cuda, monkeypatch):
+    """Parameters whose AdamW steps diverge update exactly as separate functional steps."""
+    import sr_states
+
+    module = importlib.import_module("sr_states.hip.adamw")
+    launch = module._launch
+    calls = []
+
+    def count(tables, *args):
+        calls.append(tables.nrows)
+        return launch(tables, *args)
+
+    monkeypatch.setattr(module, "_launch", count)
+    sizes = (1003, 4096 + 7, 77)
+    params = [torch.nn.Parameter(torch.linspace(-1, 1, n, device=cuda)) for n in sizes]
+    expected = [p.detach().clone() for p in params]
+    states = [[torch.zeros(n, device=cuda, dtype=torch.bfloat16) for _ in range(2)] for n in sizes]
+    opt = sr_states.AdamWHip(params, lr=0.05, seed=9)
+    generator = torch.Generator(device=cuda).manual_seed(3)
+    steps = [0, 0, 0]
+    for t in range(1, 7):
+        skip = t % 3 if t > 1 else None  # one parameter without a gradient per step
+        for k, p in enumerate(params):
+            p.grad = None if k == skip else torch.randn(p.shape, device=cuda, generator=generator) * 0.1
+        calls.clear()
+        opt.step()
+        assert calls == [len(params) - (skip is not None)]
+        for k, p in enumerate(params):
+            if k == skip:
+                continue
+            steps[k] += 1
+            sr_states.hip_adamw_step_(expected[k], p.grad, *states[k], lr=0.05, beta1=0.9, beta2=0.999,
+                                      eps=1e-8, weight_decay=1e-2, step=steps[k],
+                                      seed=sr_states.update_key(9, t, k))
+        for k, p in enumerate(params):
+            assert opt.state[p]["step"] == steps[k] if steps[k] else p not in opt.state
+            assert_bytes(p.detach(), expected[k])
+            if steps[k]:
+                assert_bytes(opt.state[p]["exp_avg"], states[k][0])
+                assert_bytes(opt.state[p]["exp_avg_sq"], states[k][1])
+    assert len(set(steps)) > 1

@@ -18,8 +18,16 @@ from contextlib import nullcontext
 import pytest
 import torch
 
+import math
+
+import numpy as np
+
 from sr_states import AdamWHip, SGDMHip, _group_walk, _lib
 from sr_states.hip import _multi_tensor
+
+
+def _f32(value):
+    return float(np.float32(value))
 
 NAMES = ("exp_avg", "exp_avg_sq")
 
@@ -40,9 +48,24 @@ def _sig(params, state, *, uses_step=True, first_index=0):
 def test_signature_is_stable_and_lists_state_entries():
     params, state = _group()
     first, second = _sig(params, state), _sig(params, state)
-    assert first[0] == second[0] and first[1] == 0
-    assert first[2] == [state[p] for p in params]
+    assert first[0] == second[0] and first[1] == 0 and first[2] is None
+    assert first[3] == [state[p] for p in params]
     assert _sig(params, state, first_index=3)[0] != first[0]
+    sgdm = _sig(params, state, uses_step=False)
+    assert sgdm[1] is None and sgdm[2] is None
+
+
+def test_mixed_steps_are_listed_not_signed():
+    """Stored steps stay out of the bytes; differing steps come back per parameter."""
+    params, state = _group()
+    uniform = _sig(params, state)
+    state[params[0]]["step"] = 4
+    state[params[2]]["step"] = 2
+    mixed = _sig(params, state)
+    assert mixed[0] == uniform[0]
+    assert mixed[1] is None and mixed[2] == [4, 0, 2]
+    params[1].grad = None
+    assert _sig(params, state)[2] == [4, 2]
 
 
 @pytest.mark.parametrize(
@@ -102,7 +125,7 @@ class _Wrapper(torch.Tensor):
         raise NotImplementedError(func)
 
 
-@pytest.mark.parametrize("case", ["missing_state", "missing_name", "tensor_step", "mixed_steps",
+@pytest.mark.parametrize("case", ["missing_state", "missing_name", "tensor_step", "negative_step",
                                   "wrapper", "meta", "not_a_tensor", "sparse_grad",
                                   "no_gradients", "huge_step"])
 def test_unvouched_groups_take_the_validating_path(case):
@@ -115,8 +138,8 @@ def test_unvouched_groups_take_the_validating_path(case):
     elif case == "tensor_step":
         for q in params:
             state[q]["step"] = torch.tensor(1.0)
-    elif case == "mixed_steps":
-        state[p]["step"] = 2
+    elif case == "negative_step":
+        state[p]["step"] = -1
     elif case == "wrapper":
         state[p]["exp_avg"] = _Wrapper(state[p]["exp_avg"])
     elif case == "meta":
@@ -152,9 +175,11 @@ def recorder(monkeypatch):
     for kind in ("adamw", "sgd"):
         module = importlib.import_module(f"sr_states.hip.{kind}")
 
-        def record(tables, dtypes, hparams, seed, rng_step, block_size, stream, _kind=kind):
+        def record(tables, dtypes, hparams, seed, rng_step, block_size, stream, row_scalars=None, *,
+                   _kind=kind):
             launches.append({"kind": _kind, "tables": tables, "dtypes": dtypes, "hparams": hparams,
-                             "seed": seed, "rng_step": rng_step, "block_size": block_size})
+                             "seed": seed, "rng_step": rng_step, "block_size": block_size,
+                             "row_scalars": row_scalars})
 
         monkeypatch.setattr(module, "_launch", record)
         monkeypatch.setattr(module, "validate_update_device", lambda *args: None)
@@ -215,14 +240,22 @@ def test_changes_after_reuse_are_validated_again(recorder, monkeypatch):
     opt.step()
     assert recorder[-1]["tables"].records["param_index"].tolist() == [1, 2]
     assert [opt.state[p]["step"] for p in params] == [4, 5, 5]
-    # Mixed stored steps split the bucket again, through the validating path.
+    # Mixed stored steps share one launch with per-row bias corrections.
     params[0].grad = torch.ones(9)
     opt.step()
-    assert [launch["tables"].nrows for launch in recorder[-2:]] == [1, 2]
-    assert [launch["hparams"].neg_step_size for launch in recorder[-2:]] == [
-        pytest.approx(-0.01 / (1 - 0.9**t)) for t in (5, 6)]
-    # An in-place resize keeps the address; the shape check still fires.
+    assert len(validations) == 5
+    merged = recorder[-1]
+    assert merged["tables"].nrows == 3
+    assert merged["row_scalars"].view(torch.float32).view(3, 2).tolist() == [
+        [_f32(-0.01 / (1 - 0.9**t)), _f32(math.sqrt(1 - 0.999**t))] for t in (5, 6, 6)]
+    # The next step reuses the plan, with every row one step further.
     opt.step()
+    assert len(validations) == 5
+    assert recorder[-1]["tables"] is merged["tables"]
+    assert recorder[-1]["row_scalars"].view(torch.float32).view(3, 2)[:, 0].tolist() == [
+        _f32(-0.01 / (1 - 0.9**t)) for t in (6, 7, 7)]
+    assert [opt.state[p]["step"] for p in params] == [6, 7, 7]
+    # An in-place resize keeps the address; the shape check still fires.
     opt.state[params[2]]["exp_avg"].resize_(3, 3)
     count = len(recorder)
     with pytest.raises(ValueError, match="shapes"):

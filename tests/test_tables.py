@@ -44,16 +44,23 @@ def item(n, index=0, step=1, *, dtype=torch.float32, offset=0, device="cpu", gra
     return p, {"m": torch.zeros(n, device=device)}, index, step, offset
 
 
-def test_buckets_split_device_dtypes_and_adamw_steps():
-    """tests/test_multi_tensor_tables.py:36-57."""
+def test_buckets_split_device_and_dtypes_and_rows_keep_their_steps():
+    """tests/test_multi_tensor_tables.py:36-57, with AdamW steps kept per row.
+
+    The reference also splits AdamW buckets by step; here a row at another
+    step stays in its dtype bucket and carries its own step.
+    """
     items = [item(0, 0), item(17, 2), item(5, 4, step=2), item(3, 5, dtype=torch.bfloat16),
              item(1, 6, grad_dtype=torch.bfloat16), item(2, 7, device="meta"), item(1, 9)]
     adamw = bucket_items(items, MOMENT, uses_step=True)
     sgdm = bucket_items(items, MOMENT, uses_step=False)
-    assert [[r.param_index for r in rows] for rows in adamw.values()] == [[2, 9], [4], [5], [6], [7]]
+    assert [[r.param_index for r in rows] for rows in adamw.values()] == [[2, 4, 9], [5], [6], [7]]
     assert [[r.param_index for r in rows] for rows in sgdm.values()] == [[2, 4, 9], [5], [6], [7]]
-    (device, dtypes, step), *_ = adamw
-    assert (device.type, dtypes, step) == ("cpu", (torch.float32,) * 3, 1)
+    first = next(iter(adamw.values()))
+    assert [(r.step, r.position) for r in first] == [(1, 1), (2, 2), (1, 6)]
+    assert [r.step for r in next(iter(sgdm.values()))] == [None] * 3
+    (device, dtypes), *_ = adamw
+    assert (device.type, dtypes) == ("cpu", (torch.float32,) * 3)
 
 
 def test_records_and_tile_map_layout():
@@ -93,17 +100,25 @@ def test_table_cache_reuse_and_refresh():
     """tests/test_multi_tensor_tables.py:60-121: step-invariant tables, refresh on change."""
     items = [item(n, i, offset=2**32 - 20 + i) for i, n in enumerate((1, 600, 1024, 1025))]
     cache = GroupTableCache()
-    ((_, _, _, first),) = cache.prepare(bucket_items(items, MOMENT, uses_step=True), 128)
+
+    def tables(rows, block):
+        (launch,) = cache.prepare(bucket_items(rows, MOMENT, uses_step=True), block)
+        return launch.steps, launch.tables
+
+    steps, first = tables(items, 128)
     assert first.tile_rows.tolist() == [0, 1, 1, 2, 2, 3, 3, 3]  # 512-element tiles
-    ((_, step, _, same),) = cache.prepare(
-        bucket_items([(*row[:3], 2, row[-1]) for row in items], MOMENT, uses_step=True), 128)
-    assert step == 2 and same is first
-    ((_, _, _, resized),) = cache.prepare(bucket_items(items, MOMENT, uses_step=True), 256)
+    assert steps == 1
+    steps, same = tables([(*row[:3], 2, row[-1]) for row in items], 128)
+    assert steps == 2 and same is first
+    # Rows at different steps share the launch and the tables.
+    steps, mixed = tables([(*row[:3], 2 + (k == 2), row[-1]) for k, row in enumerate(items)], 128)
+    assert steps == (2, 2, 3, 2) and mixed is first
+    steps, resized = tables(items, 256)
     assert resized is not first and resized.tile_rows.tolist() == [0, 1, 2, 3, 3]
     # Same layout, a new gradient address: records rebuilt, tile map reused.
     p = items[1][0]
     p.grad = torch.zeros_like(p.grad)
-    ((_, _, _, moved),) = cache.prepare(bucket_items(items, MOMENT, uses_step=True), 256)
+    steps, moved = tables(items, 256)
     assert moved is not resized and moved.device_tile_rows is resized.device_tile_rows
     assert moved.records["ptr"][1][1] == p.grad.data_ptr()
 
@@ -174,9 +189,11 @@ def recorder(monkeypatch):
     for kind in ("adamw", "sgd"):
         module = importlib.import_module(f"sr_states.hip.{kind}")
 
-        def record(tables, dtypes, hparams, seed, rng_step, block_size, stream, _kind=kind):
+        def record(tables, dtypes, hparams, seed, rng_step, block_size, stream, row_scalars=None, *,
+                   _kind=kind):
             launches.append({"kind": _kind, "tables": tables, "dtypes": dtypes, "hparams": hparams,
-                             "seed": seed, "rng_step": rng_step, "block_size": block_size})
+                             "seed": seed, "rng_step": rng_step, "block_size": block_size,
+                             "row_scalars": row_scalars})
 
         monkeypatch.setattr(module, "_launch", record)
         monkeypatch.setattr(module, "validate_update_device", lambda *args: None)
