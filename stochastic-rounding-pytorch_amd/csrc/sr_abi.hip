@@ -200,10 +200,9 @@ int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, const float* r
   a.row_scalars = row_scalars;
   a.total_tiles = total_tiles;
   a.s = adamw_scalars(*hp);
-  a.seed_lo = static_cast<uint32_t>(seed);
-  a.seed_hi = static_cast<uint32_t>(seed >> 32);
-  a.step_lo = static_cast<uint32_t>(rng_step);
-  a.step_hi = static_cast<uint32_t>(rng_step >> 32);
+  a.key_prefix = sr::update_key_prefix(static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32),
+                                       static_cast<uint32_t>(rng_step),
+                                       static_cast<uint32_t>(rng_step >> 32));
   return launch(tables().adamw[pi][gi][me][ve], block_size, total_tiles, &a, stream);
 }
 
@@ -256,10 +255,9 @@ int sr_sgdm_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint
   a.tile_rows = tile_rows;
   a.total_tiles = total_tiles;
   a.s = {hp->momentum, hp->neg_lr};
-  a.seed_lo = static_cast<uint32_t>(seed);
-  a.seed_hi = static_cast<uint32_t>(seed >> 32);
-  a.step_lo = static_cast<uint32_t>(rng_step);
-  a.step_hi = static_cast<uint32_t>(rng_step >> 32);
+  a.key_prefix = sr::update_key_prefix(static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32),
+                                       static_cast<uint32_t>(rng_step),
+                                       static_cast<uint32_t>(rng_step >> 32));
   return launch(tables().sgdm[pi][gi][ue], block_size, total_tiles, &a, stream);
 }
 

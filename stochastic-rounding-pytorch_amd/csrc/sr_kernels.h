@@ -57,7 +57,7 @@ struct AdamWArgs {
   sr_row inline_row;
   AdamWScalars s;
   uint32_t total_tiles;
-  uint32_t seed_lo, seed_hi, step_lo, step_hi;
+  uint32_t key_prefix;  // update_key_prefix(seed, rng_step), computed by the host
 };
 
 struct SgdmArgs {
@@ -66,7 +66,7 @@ struct SgdmArgs {
   sr_row inline_row;
   SgdmScalars s;
   uint32_t total_tiles;
-  uint32_t seed_lo, seed_hi, step_lo, step_hi;
+  uint32_t key_prefix;  // update_key_prefix(seed, rng_step), computed by the host
 };
 
 struct CastArgs {
@@ -195,7 +195,7 @@ template <class Args>
 __device__ __forceinline__ uint32_t row_key(const Args& a, const sr_row& r) {
   return (r.flags & SR_ROW_KEYED)
              ? r.param_index
-             : update_key(a.seed_lo, a.seed_hi, a.step_lo, a.step_hi, r.param_index);
+             : update_key_from_prefix(a.key_prefix, r.param_index);
 }
 
 // ---------------------------------------------------------------------------

@@ -38,13 +38,23 @@ SR_HD uint32_t h32(uint32_t x) {
 
 // Update key of one parameter at one optimizer RNG step.  The seed and step
 // enter as their low and high 32-bit words (sr_states/_hash.py:18-23).
-SR_HD uint32_t update_key(uint32_t seed_lo, uint32_t seed_hi, uint32_t step_lo,
-                          uint32_t step_hi, uint32_t param_index) {
+// The first four rounds depend only on (seed, step), so a launch computes
+// them once (update_key_prefix) and each row adds its parameter index.
+SR_HD uint32_t update_key_prefix(uint32_t seed_lo, uint32_t seed_hi, uint32_t step_lo,
+                                 uint32_t step_hi) {
   uint32_t key = h32(seed_lo ^ kKeySalt);
   key = h32(key ^ seed_hi);
   key = h32(key ^ step_lo);
-  key = h32(key ^ step_hi);
-  return h32(key ^ param_index);
+  return h32(key ^ step_hi);
+}
+
+SR_HD uint32_t update_key_from_prefix(uint32_t prefix, uint32_t param_index) {
+  return h32(prefix ^ param_index);
+}
+
+SR_HD uint32_t update_key(uint32_t seed_lo, uint32_t seed_hi, uint32_t step_lo,
+                          uint32_t step_hi, uint32_t param_index) {
+  return update_key_from_prefix(update_key_prefix(seed_lo, seed_hi, step_lo, step_hi), param_index);
 }
 
 // Per-state counter base (sr_states/_hash.py:26-28).
