@@ -346,3 +346,14 @@ def test_buckets_are_tiled_at_their_lane_width(recorder):
         tiles = -(-n // (block * lanes))
         assert launch["tables"].total_tiles == tiles
         assert launch["tables"].records["tile_end"].tolist() == [tiles]
+
+
+def test_tile_limit_is_the_launch_grid():
+    """A bucket may not need more workgroups than one launch can hold."""
+    from sr_states.hip._multi_tensor import MAX_TILES
+
+    tile = 1024
+    assert build_tile_rows([(tile, 0, 0), (1, 1, 0)], tile).tolist() == [0, 1]
+    # One tile past the limit fails before anything is allocated.
+    with pytest.raises(ValueError, match="at most"):
+        build_tile_rows([(MAX_TILES * tile, 0, 0), (1, 1, 0)], tile)
