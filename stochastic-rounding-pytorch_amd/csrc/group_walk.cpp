@@ -4,24 +4,35 @@
 // The reference validates and buckets every tensor of a group on every step
 // (sr_states/triton/_multi_tensor.py:22-34 and :61-88).  The row tables only
 // change when a layout, an address or the set of parameters with gradients
-// changes, so this module condenses exactly those facts into one byte string
-// per step.  The Python side runs the full validation and rebuilds the tables
-// whenever the string differs from the one recorded at the last fully
-// validated step; when it is equal, nothing the validation or the tables
-// depend on has changed and the recorded launches are reused.
+// changes, so this module condenses exactly those facts for the Python side,
+// which runs the full validation whenever they differ from those of an
+// earlier fully validated step.  Gradients are reported apart from the rest:
+// training loops free them every step and get them back at varying
+// addresses, and a new gradient address only needs its table column patched
+// and the overlap rule checked again (spans_disjoint).
 //
 // group_signature(params, state, state_names, uses_step, first_index)
-//     -> (bytes, step, steps, entries) or None
-//   Each tensor contributes its Python type, so a validated step vouches only
-//   for the types it saw.  None means "take the validating path": an object
-//   that is not a tensor, a missing state, a non-strided tensor, one with
-//   elements but no memory (wrapper subclasses), a stored step that is not a
-//   non-negative int, or no parameter with a gradient.  Stored steps are not
-//   part of the bytes.  When uses_step is true and every parameter with a
-//   gradient stores the same step (0 when absent), ``step`` is that value and
-//   ``steps`` is None; when they differ, ``step`` is None and ``steps`` lists
-//   them in group order.  Both are None when uses_step is false.  ``entries``
-//   lists the state dict of every parameter with a gradient, in group order.
+//     -> (layout, step, steps, entries, gradients, spans) or None
+//   ``layout`` (bytes) fixes every tensor's Python type, element count, dtype,
+//   device, contiguity and sizes, every parameter's and state's address, and
+//   which parameters have gradients; gradient addresses are left out.  A
+//   validated step vouches only for the types it saw.  None means "take the
+//   validating path": an object that is not a tensor, a missing state, a
+//   non-strided tensor, one with elements but no memory (wrapper
+//   subclasses), a stored step that is not a non-negative int, or no
+//   parameter with a gradient.  When uses_step is true and every parameter
+//   with a gradient stores the same step (0 when absent), ``step`` is that
+//   value and ``steps`` is None; when they differ, ``step`` is None and
+//   ``steps`` lists them in group order.  Both are None when uses_step is
+//   false.  ``entries`` lists the state dict of every parameter with a
+//   gradient, in group order; ``gradients`` (bytes) their gradients'
+//   addresses as int64; ``spans`` (bytes) one (device, start, end, written)
+//   int64 quadruple per tensor with elements.
+//
+// spans_disjoint(spans) -> bool
+//   The overlap rule of the validating path (triton/_optimizer.py:38-49):
+//   per device, every written span is disjoint from every other span;
+//   gradients are only read and may share memory with each other.
 //
 // set_steps(entries, value)
 //   entry["step"] = value for every dict in the list ``entries``.
@@ -30,6 +41,9 @@
 #include <Python.h>
 #include <torch/csrc/autograd/python_variable.h>
 
+#include <algorithm>
+#include <array>
+#include <climits>
 #include <cstdint>
 #include <vector>
 
@@ -38,27 +52,45 @@ namespace {
 PyObject* g_grad = nullptr;  // interned "grad"
 PyObject* g_step = nullptr;  // interned "step"
 
-// Appends the words that fix one tensor's view: Python type, address, element
-// count, dtype, device, contiguity, rank and sizes.  False when the object is
-// not a tensor or has no strided memory to describe.
-bool describe(PyObject* obj, std::vector<int64_t>& words) {
+// Everything one walk collects.
+struct Walk {
+  std::vector<int64_t> words;      // the layout signature
+  std::vector<int64_t> gradients;  // gradient address per parameter with a gradient
+  std::vector<int64_t> spans;      // (device, start, end, written) per tensor with elements
+  std::vector<int64_t> steps;      // stored step per parameter with a gradient
+};
+
+// Appends the words that fix one tensor's view: Python type, address (unless
+// it is a gradient, whose address goes to w.gradients), element count, dtype,
+// device, contiguity, rank and sizes; and the tensor's byte span.  False when
+// the object is not a tensor or has no strided memory to describe.
+bool describe(PyObject* obj, Walk& w, bool gradient) {
   if (!THPVariable_Check(obj)) return false;
   try {
     const at::Tensor& t = THPVariable_Unpack(obj);
     if (!t.defined() || t.layout() != at::kStrided || !t.has_storage()) return false;
     const auto sizes = t.sizes();
     const at::Device device = t.device();
-    const auto address = reinterpret_cast<intptr_t>(t.data_ptr());
-    if (address == 0 && t.numel() != 0) return false;
-    words.push_back(static_cast<int64_t>(reinterpret_cast<intptr_t>(Py_TYPE(obj))));
-    words.push_back(static_cast<int64_t>(address));
-    words.push_back(t.numel());
-    words.push_back(static_cast<int64_t>(t.scalar_type()) |
-                    static_cast<int64_t>(device.type()) << 8 |
-                    static_cast<int64_t>(static_cast<uint8_t>(device.index())) << 16 |
-                    static_cast<int64_t>(t.is_contiguous()) << 24 |
-                    static_cast<int64_t>(sizes.size()) << 32);
-    for (int64_t s : sizes) words.push_back(s);
+    const auto address = static_cast<int64_t>(reinterpret_cast<intptr_t>(t.data_ptr()));
+    const int64_t numel = t.numel();
+    if (address == 0 && numel != 0) return false;
+    const int64_t device_key =
+        static_cast<int64_t>(device.type()) << 8 | static_cast<uint8_t>(device.index());
+    w.words.push_back(static_cast<int64_t>(reinterpret_cast<intptr_t>(Py_TYPE(obj))));
+    if (gradient) {
+      w.gradients.push_back(address);
+    } else {
+      w.words.push_back(address);
+    }
+    w.words.push_back(numel);
+    w.words.push_back(static_cast<int64_t>(t.scalar_type()) | device_key << 8 |
+                      static_cast<int64_t>(t.is_contiguous()) << 24 |
+                      static_cast<int64_t>(sizes.size()) << 32);
+    for (int64_t s : sizes) w.words.push_back(s);
+    if (numel != 0) {
+      const int64_t end = address + numel * static_cast<int64_t>(t.element_size());
+      w.spans.insert(w.spans.end(), {device_key, address, end, gradient ? 0 : 1});
+    }
     return true;
   } catch (...) {
     return false;
@@ -85,19 +117,19 @@ struct Ref {
   ~Ref() { Py_XDECREF(obj); }
 };
 
-// One parameter with a gradient: its words and its stored step.
+// One parameter with a gradient: its words, spans and stored step.
 bool walk_parameter(PyObject* parameter, PyObject* gradient, PyObject* state, PyObject* names,
-                    bool uses_step, std::vector<int64_t>& words, int64_t& step, PyObject* entries) {
+                    bool uses_step, Walk& w, int64_t& step, PyObject* entries) {
   PyObject* entry = parameter_state(state, parameter);
   if (entry == nullptr) return false;
   Ref hold_entry(entry);
   Py_INCREF(entry);
   if (PyList_Append(entries, entry) != 0) return false;
-  words.push_back(2 + PyTuple_GET_SIZE(names));
-  if (!describe(parameter, words) || !describe(gradient, words)) return false;
+  w.words.push_back(2 + PyTuple_GET_SIZE(names));
+  if (!describe(parameter, w, false) || !describe(gradient, w, true)) return false;
   for (Py_ssize_t k = 0; k < PyTuple_GET_SIZE(names); ++k) {
     PyObject* tensor = PyDict_GetItemWithError(entry, PyTuple_GET_ITEM(names, k));
-    if (tensor == nullptr || !describe(tensor, words)) return false;
+    if (tensor == nullptr || !describe(tensor, w, false)) return false;
   }
   step = 0;
   if (!uses_step) return true;
@@ -110,8 +142,8 @@ bool walk_parameter(PyObject* parameter, PyObject* gradient, PyObject* state, Py
 }
 
 // The walk proper; returns false for "take the validating path".
-bool walk(PyObject* params, PyObject* state, PyObject* names, bool uses_step,
-          std::vector<int64_t>& words, std::vector<int64_t>& steps, PyObject* entries) {
+bool walk(PyObject* params, PyObject* state, PyObject* names, bool uses_step, Walk& w,
+          PyObject* entries) {
   for (Py_ssize_t i = 0; i < PyList_GET_SIZE(params); ++i) {
     PyObject* parameter = PyList_GET_ITEM(params, i);
     Ref hold_parameter(parameter);
@@ -120,16 +152,21 @@ bool walk(PyObject* params, PyObject* state, PyObject* names, bool uses_step,
     Ref gradient(PyObject_GetAttr(parameter, g_grad));
     if (gradient.obj == nullptr) return false;
     if (gradient.obj == Py_None) {
-      words.push_back(-1);
+      w.words.push_back(-1);
       continue;
     }
     int64_t step = 0;
-    if (!walk_parameter(parameter, gradient.obj, state, names, uses_step, words, step, entries)) {
+    if (!walk_parameter(parameter, gradient.obj, state, names, uses_step, w, step, entries)) {
       return false;
     }
-    steps.push_back(step);
+    w.steps.push_back(step);
   }
-  return !steps.empty();
+  return !w.steps.empty();
+}
+
+PyObject* as_bytes(const std::vector<int64_t>& v) {
+  return PyBytes_FromStringAndSize(reinterpret_cast<const char*>(v.data()),
+                                   static_cast<Py_ssize_t>(v.size() * sizeof(int64_t)));
 }
 
 PyObject* group_signature(PyObject*, PyObject* args) {
@@ -140,17 +177,18 @@ PyObject* group_signature(PyObject*, PyObject* args) {
                         &PyTuple_Type, &names, &uses_step, &first_index)) {
     return nullptr;
   }
-  std::vector<int64_t> words;
-  words.reserve(4 + PyList_GET_SIZE(params) * (1 + 7 * (2 + PyTuple_GET_SIZE(names))));
-  words.push_back(first_index);
-  words.push_back(PyList_GET_SIZE(params));
-  std::vector<int64_t> steps;
+  Walk w;
+  const Py_ssize_t tensors = PyList_GET_SIZE(params) * (2 + PyTuple_GET_SIZE(names));
+  w.words.reserve(4 + PyList_GET_SIZE(params) + 7 * tensors);
+  w.spans.reserve(4 * tensors);
+  w.words.push_back(first_index);
+  w.words.push_back(PyList_GET_SIZE(params));
   bool found = false;
   Ref entries(PyList_New(0));
   if (entries.obj == nullptr) return nullptr;
   Py_INCREF(params);  // the walk may run Python code (Tensor.__hash__)
   try {
-    found = walk(params, state, names, uses_step != 0, words, steps, entries.obj);
+    found = walk(params, state, names, uses_step != 0, w, entries.obj);
   } catch (...) {
     found = false;
   }
@@ -159,6 +197,7 @@ PyObject* group_signature(PyObject*, PyObject* args) {
     PyErr_Clear();
     Py_RETURN_NONE;
   }
+  const std::vector<int64_t>& steps = w.steps;
   bool uniform = true;
   for (int64_t s : steps) uniform = uniform && s == steps[0];
   Ref common(nullptr), listed(nullptr);
@@ -178,9 +217,36 @@ PyObject* group_signature(PyObject*, PyObject* args) {
     }
   }
   if (common.obj == nullptr || listed.obj == nullptr) return nullptr;
-  return Py_BuildValue("(y#OOO)", reinterpret_cast<const char*>(words.data()),
-                       static_cast<Py_ssize_t>(words.size() * sizeof(int64_t)), common.obj,
-                       listed.obj, entries.obj);
+  Ref layout(as_bytes(w.words)), gradients(as_bytes(w.gradients)), spans(as_bytes(w.spans));
+  if (layout.obj == nullptr || gradients.obj == nullptr || spans.obj == nullptr) return nullptr;
+  return PyTuple_Pack(6, layout.obj, common.obj, listed.obj, entries.obj, gradients.obj,
+                      spans.obj);
+}
+
+PyObject* spans_disjoint(PyObject*, PyObject* args) {
+  const char* data;
+  Py_ssize_t size;
+  if (!PyArg_ParseTuple(args, "y#", &data, &size)) return nullptr;
+  if (size % (4 * sizeof(int64_t)) != 0) {
+    PyErr_SetString(PyExc_ValueError, "spans must hold (device, start, end, written) quadruples");
+    return nullptr;
+  }
+  std::vector<std::array<int64_t, 4>> spans(static_cast<size_t>(size) / (4 * sizeof(int64_t)));
+  std::copy_n(data, size, reinterpret_cast<char*>(spans.data()));
+  // Sorted by device, then as the validating path sorts (start, end, written).
+  std::sort(spans.begin(), spans.end());
+  int64_t device = 0, max_end = 0, max_write_end = 0;
+  for (size_t k = 0; k < spans.size(); ++k) {
+    const auto& [dev, start, end, written] = spans[k];
+    if (k == 0 || dev != device) {
+      device = dev;
+      max_end = max_write_end = INT64_MIN;
+    }
+    if (start < (written ? max_end : max_write_end)) Py_RETURN_FALSE;
+    max_end = std::max(max_end, end);
+    if (written) max_write_end = std::max(max_write_end, end);
+  }
+  Py_RETURN_TRUE;
 }
 
 PyObject* set_steps(PyObject*, PyObject* args) {
@@ -198,6 +264,7 @@ PyObject* set_steps(PyObject*, PyObject* args) {
 PyMethodDef kMethods[] = {
     {"group_signature", group_signature, METH_VARARGS,
      "group_signature(params, state, state_names, uses_step, first_index)"},
+    {"spans_disjoint", spans_disjoint, METH_VARARGS, "spans_disjoint(spans) -> bool"},
     {"set_steps", set_steps, METH_VARARGS, "set_steps(entries, value)"},
     {nullptr, nullptr, 0, nullptr},
 };

@@ -103,7 +103,61 @@ def test_every_table_input_changes_the_signature(change):
             pass
         state[p]["exp_avg"] = state[p]["exp_avg"].as_subclass(Sub)
     after = _sig(params, state)
-    assert after is not None and (after[0] != before[0] or after[1] != before[1])
+    assert after is not None
+    # Layout, stored step or gradient addresses: one of them must differ.
+    assert (after[0], after[1], after[4]) != (before[0], before[1], before[4])
+    if change == "grad_address":
+        assert after[0] == before[0], "gradient addresses stay out of the layout"
+
+
+def test_gradients_and_spans_describe_the_current_tensors():
+    params, state = _group()
+    sig = _sig(params, state)
+    gradients = np.frombuffer(sig[4], dtype=np.int64).tolist()
+    assert gradients == [p.grad.data_ptr() for p in params]
+    spans = np.frombuffer(sig[5], dtype=np.int64).reshape(-1, 4)
+    expected = []
+    for p in params:
+        for t, written in ((p, 1), (p.grad, 0), (state[p]["exp_avg"], 1), (state[p]["exp_avg_sq"], 1)):
+            expected.append([t.data_ptr(), t.data_ptr() + t.nbytes, written])
+    assert spans[:, 1:].tolist() == expected
+    assert len(set(spans[:, 0].tolist())) == 1  # one device
+    assert _group_walk.spans_disjoint(sig[5])
+
+
+@pytest.mark.parametrize("alias", ["grads_share", "grad_is_state", "state_overlaps_param", "other_device"])
+def test_spans_disjoint_follows_the_validating_overlap_rule(alias):
+    """triton/_optimizer.py:38-49: gradients may share memory; written spans may not overlap."""
+    from sr_states.hip._optimizer import validate_no_overlap
+
+    params, state = _group()
+    if alias == "grads_share":
+        shared = torch.zeros(5)
+        params[0].grad, params[1].grad = shared, shared
+    elif alias == "grad_is_state":
+        # One parameter's gradient (read) shares bytes with another's state (written).
+        base = torch.zeros(10)
+        params[1].grad = base[:5]
+        state[params[2]]["exp_avg"] = base.view(torch.bfloat16)[:5]
+    elif alias == "state_overlaps_param":
+        base = torch.zeros(8)
+        params[0].data = base[:5]
+        state[params[0]]["exp_avg_sq"] = base[3:].view(torch.bfloat16)[:5]
+    sig = _sig(params, state)
+    spans = np.frombuffer(sig[5], dtype=np.int64).reshape(-1, 4)
+    if alias == "other_device":
+        # The same addresses on another device never overlap.
+        moved = spans.copy()
+        moved[::2, 0] += 1
+        assert _group_walk.spans_disjoint(moved.tobytes())
+        return
+    try:
+        validate_no_overlap([(int(a), int(b), bool(w)) for _, a, b, w in spans])
+        python_ok = True
+    except ValueError:
+        python_ok = False
+    assert _group_walk.spans_disjoint(sig[5]) is python_ok
+    assert python_ok is (alias == "grads_share")
 
 
 def test_in_place_resize_keeps_the_address_but_changes_the_signature():
@@ -229,32 +283,45 @@ def test_changes_after_reuse_are_validated_again(recorder, monkeypatch):
     for _ in range(3):
         opt.step()
     assert len(validations) == 2
-    # A new gradient tensor moves an address: the tables are rebuilt.
+    # A new gradient tensor moves an address: its record column is patched
+    # without a validation; the tile map is shared.
+    before = recorder[-1]["tables"]
     params[1].grad = torch.full_like(params[1], 2.0)
     opt.step()
-    assert len(validations) == 3
-    records = recorder[-1]["tables"].records
-    assert int(records["ptr"][1][1]) == params[1].grad.data_ptr()
+    assert len(validations) == 2
+    patched = recorder[-1]["tables"]
+    assert patched is not before and patched.device_tile_rows is before.device_tile_rows
+    assert int(patched.records["ptr"][1][1]) == params[1].grad.data_ptr()
+    assert patched.records["ptr"][[0, 2]].tolist() == before.records["ptr"][[0, 2]].tolist()
+    # A gradient at an address that overlaps a written buffer keeps the
+    # layout, but fails the overlap rule: the validating path reports it.
+    count = len(recorder)
+    params[1].grad = params[2].detach()
+    with pytest.raises(ValueError, match="overlap"):
+        opt.step()
+    assert len(recorder) == count and len(validations) == 3
+    params[1].grad = torch.full_like(params[1], 2.0)
+    opt.step()
     # A parameter without a gradient keeps its index but leaves the bucket.
     params[0].grad = None
     opt.step()
     assert recorder[-1]["tables"].records["param_index"].tolist() == [1, 2]
-    assert [opt.state[p]["step"] for p in params] == [4, 5, 5]
+    assert [opt.state[p]["step"] for p in params] == [5, 6, 6]
     # Mixed stored steps share one launch with per-row bias corrections.
     params[0].grad = torch.ones(9)
     opt.step()
-    assert len(validations) == 5
+    validated = len(validations)
     merged = recorder[-1]
     assert merged["tables"].nrows == 3
     assert merged["row_scalars"].view(torch.float32).view(3, 2).tolist() == [
-        [_f32(-0.01 / (1 - 0.9**t)), _f32(math.sqrt(1 - 0.999**t))] for t in (5, 6, 6)]
+        [_f32(-0.01 / (1 - 0.9**t)), _f32(math.sqrt(1 - 0.999**t))] for t in (6, 7, 7)]
     # The next step reuses the plan, with every row one step further.
     opt.step()
-    assert len(validations) == 5
+    assert len(validations) == validated
     assert recorder[-1]["tables"] is merged["tables"]
     assert recorder[-1]["row_scalars"].view(torch.float32).view(3, 2)[:, 0].tolist() == [
-        _f32(-0.01 / (1 - 0.9**t)) for t in (6, 7, 7)]
-    assert [opt.state[p]["step"] for p in params] == [6, 7, 7]
+        _f32(-0.01 / (1 - 0.9**t)) for t in (7, 8, 8)]
+    assert [opt.state[p]["step"] for p in params] == [7, 8, 8]
     # An in-place resize keeps the address; the shape check still fires.
     opt.state[params[2]]["exp_avg"].resize_(3, 3)
     count = len(recorder)
@@ -317,3 +384,23 @@ def test_checkpoint_round_trip_with_reuse_matches_fresh_validation(recorder):
     assert first["seed"] == second["seed"] == 4
     assert first["hparams"].neg_step_size == second["hparams"].neg_step_size
     assert first["tables"].records["param_index"].tolist() == [0, 1]
+
+
+def test_alternating_gradient_addresses_reuse_their_own_records(recorder, monkeypatch):
+    """Gradients that come back at alternating addresses (set_to_none loops) hit the cache."""
+    validations = _spy(monkeypatch)
+    params = [torch.nn.Parameter(torch.ones(33)) for _ in range(3)]
+    grads = [[torch.full((33,), 0.1 * (k + 1)) for _ in params] for k in range(2)]
+    opt = AdamWHip(params, lr=0.01)
+    for step in range(10):
+        for p, g in zip(params, grads[step % 2]):
+            p.grad = g
+        opt.step()
+        records = recorder[-1]["tables"].records
+        assert [int(ptr[1]) for ptr in records["ptr"]] == [g.data_ptr() for g in grads[step % 2]]
+    # Step 1 allocates the states and step 2 validates the layout; the other
+    # address set is patched in once and both variants are reused after that.
+    assert len(validations) == 2
+    assert [opt.state[p]["step"] for p in params] == [10, 10, 10]
+    tables = {id(launch["tables"]) for launch in recorder[1:]}
+    assert len(tables) == 2
