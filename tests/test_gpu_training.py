@@ -85,7 +85,9 @@ def test_sr_states_train_like_fp32_states(cuda, kind, monkeypatch):
     # FP32 states' loss (AdamW 0.0279, SGD 0.1319 from 0.902).
     assert sr[-1] < drop * sr[0]
     assert abs(sr[-1] - full[-1]) <= 0.02 * full[-1]
-    # New gradient tensors each step.  After a few warm-up steps the caching
-    # allocator hands them out at two alternating sets of addresses, and each
-    # set's validated launches are reused.
-    assert validations_sr <= 16
+    # New gradient tensors each step, at addresses the caching allocator
+    # varies (8 sets during warm-up, then an alternating pair, on MI355X).
+    # Only the first step (which allocates the states) and the second (which
+    # validates the layout) take the validating path; later steps patch or
+    # reuse the gradient columns.
+    assert validations_sr == 2
