@@ -280,6 +280,12 @@ def cpu_baseline(spec, target_seconds: float = 12.0):
         return cls([group])
 
     threads = torch.get_num_threads()
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as info:
+            model = next(line.split(":", 1)[1].strip() for line in info if line.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
     median, count = _median_step_seconds(make(n), target_seconds * 2 / 3)
     n1 = max(n // 4, 1)
     torch.set_num_threads(1)
@@ -295,7 +301,7 @@ def cpu_baseline(spec, target_seconds: float = 12.0):
         "value_one_thread": n1 / median1,
         "sample": f"{count} eager steps of one {n}-element tensor of the workload at {threads} "
         f"threads (median {median * 1e3:.1f} ms) and {count1} steps of {n1} elements at 1 thread "
-        f"(median {median1 * 1e3:.1f} ms); torch {torch.__version__}, "
+        f"(median {median1 * 1e3:.1f} ms); {model}, torch {torch.__version__}, "
         f"{torch.backends.cpu.get_cpu_capability()}, {os.cpu_count()} host CPUs visible",
     }
 
