@@ -361,3 +361,27 @@ def test_rows_at_different_steps_share_one_launch(cuda, monkeypatch):
                 assert_bytes(opt.state[p]["exp_avg"], states[k][0])
                 assert_bytes(opt.state[p]["exp_avg_sq"], states[k][1])
     assert len(set(steps)) > 1
+
+
+@pytest.mark.parametrize("kind", ["adamw", "sgd"])
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")  # nothing was launched: the point
+def test_graph_capture_is_refused_before_any_launch(cuda, kind):
+    """Replaying a captured step would repeat its scalars; the optimizers refuse capture."""
+    import sr_states
+
+    cls = sr_states.AdamWHip if kind == "adamw" else sr_states.SGDMHip
+    p = torch.nn.Parameter(torch.ones(1000, device=cuda))
+    p.grad = torch.full_like(p, 0.5)
+    opt = cls([p], lr=0.01)
+    opt.step()
+    before = p.detach().clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="cannot be captured"):
+        with torch.cuda.graph(graph):
+            opt.step()
+    torch.cuda.synchronize()
+    assert_bytes(p.detach(), before)
+    opt.step()  # eager steps still work after the refused capture
+    torch.cuda.synchronize()
+    assert not torch.equal(p.detach(), before)
