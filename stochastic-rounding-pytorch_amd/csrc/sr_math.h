@@ -118,6 +118,24 @@ SR_HD uint32_t bf16_sr_bits(uint32_t b, uint32_t hash) {
   return (nan ? quieted : rounded) >> 16;
 }
 
+// The same rounding with gfx950's stochastic convert.  v_cvt_sr_bf16_f32
+// adds the upper 16 bits of its random operand below the BF16 mantissa and
+// truncates, so it equals bf16_sr_bits when given the 16 random bits in the
+// upper half.  Checked exactly, NaN payloads included, over every FP32 input
+// at the random values where the decision flips, and over every pair of low
+// input half and random value for the special and ordinary upper halves
+// (tests/native/bf16_sr_check.hip).  Host builds use bf16_sr_bits.
+SR_HD uint32_t bf16_sr(uint32_t b, uint32_t hash) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 out =
+      __builtin_amdgcn_cvt_sr_bf16_f32(bf16x2{}, __builtin_bit_cast(float, b), hash << 16, false);
+  return __builtin_bit_cast(uint32_t, out) & 0xFFFFu;
+#else
+  return bf16_sr_bits(b, hash);
+#endif
+}
+
 // FP32 -> BF16 round to nearest, ties to even (torch's Tensor.to(bfloat16)).
 SR_HD uint32_t bf16_rn_bits(uint32_t b) {
   if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
@@ -201,7 +219,7 @@ SR_HD uint32_t encode(float x, uint32_t counter) {
   } else if constexpr (ENC == ENC_BF16_RN) {
     return bf16_rn_bits(b);
   } else if constexpr (ENC == ENC_BF16_SR) {
-    return bf16_sr_bits(b, h32(counter));
+    return bf16_sr(b, h32(counter));
   } else if constexpr (ENC == ENC_F16_RN) {
     return minifloat_bits<F16, false>(b, 0);
   } else if constexpr (ENC == ENC_F16_SR) {

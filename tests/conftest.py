@@ -25,6 +25,14 @@ def pytest_configure(config):
     # Markers are registered in pytest.ini.
     built = (PACKAGE_DIR / "sr_states").glob("_group_walk*.so")
     library = PACKAGE_DIR / "sr_states" / "libsr_states_hip.so"
+    check = ROOT / "tests" / "native" / "libbf16_sr_check.so"
+    if not check.exists() and not torch.cuda.is_available():
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("sr_checks", ROOT / "tests" / "native" / "build_checks.py")
+        module = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(module)
+        module.build()
     if (not library.exists() or not any(built)) and not torch.cuda.is_available():
         # Only a CPU checkout builds here; GPU runs use the prebuilt library.
         import importlib.util

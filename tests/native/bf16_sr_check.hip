@@ -1,0 +1,83 @@
+// Exhaustive device check of the BF16 stochastic-rounding encoder: the
+// product's device path sr::bf16_sr (gfx950's v_cvt_sr_bf16_f32) against the
+// portable formula sr::bf16_sr_bits, compared bit for bit, NaN payloads
+// included.
+//   sweep 1: every FP32 input with five random values each: the two values
+//            where its rounding decision flips, 0, 0xFFFF and a hashed value;
+//   sweep 2: for twelve upper halves (zeros, subnormals, ordinary values, the
+//            largest finite value, Inf and NaN patterns, both signs), every
+//            pair of low input half and 16-bit random value.
+// Built by __graft_entry__.build() into tests/native/libbf16_sr_check.so and
+// run by tests/test_gpu_bf16_sr_check.py.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../stochastic-rounding-pytorch_amd/csrc/sr_math.h"
+
+namespace {
+
+__device__ unsigned long long wave_sum(unsigned long long x) {
+  for (int offset = 32; offset > 0; offset >>= 1) x += __shfl_xor(x, offset, 64);
+  return x;
+}
+
+__device__ void add(unsigned long long* counters, unsigned long long mismatches,
+                    unsigned long long checks) {
+  const unsigned long long m = wave_sum(mismatches), c = wave_sum(checks);
+  if ((threadIdx.x & 63) == 0) {
+    if (m) atomicAdd(&counters[0], m);
+    atomicAdd(&counters[1], c);
+  }
+}
+
+// One launch covers 2^31 inputs starting at `base`.
+__global__ void every_input(uint32_t base, unsigned long long* counters) {
+  const uint32_t b = base + blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t lo = b & 0xFFFFu;
+  const uint32_t randoms[5] = {(0x10000u - lo) & 0xFFFFu, (0xFFFFu - lo) & 0xFFFFu, 0u, 0xFFFFu,
+                               sr::h32(b ^ 0x5bd1e995u)};
+  unsigned long long mismatches = 0;
+  for (uint32_t r : randoms) mismatches += sr::bf16_sr(b, r) != sr::bf16_sr_bits(b, r);
+  add(counters, mismatches, 5);
+}
+
+// One launch covers 2^15 random values x 2^16 low halves for upper half `hi`;
+// each thread also takes the random value with bit 15 set.
+__global__ void every_pair(uint32_t hi, unsigned long long* counters) {
+  const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t b = (hi << 16) | (idx & 0xFFFFu);
+  const uint32_t r = (idx >> 16) & 0x7FFFu;
+  unsigned long long mismatches = 0;
+  for (uint32_t random : {r, r | 0x8000u}) {
+    mismatches += sr::bf16_sr(b, random) != sr::bf16_sr_bits(b, random);
+  }
+  add(counters, mismatches, 2);
+}
+
+}  // namespace
+
+// counters_host[0] = mismatches, [1] = comparisons.  Returns 0 or a hipError_t.
+extern "C" int sr_check_bf16_sr(unsigned long long* counters_host) {
+  unsigned long long* counters = nullptr;
+  hipError_t err = hipMalloc(&counters, 2 * sizeof(unsigned long long));
+  if (err == hipSuccess) err = hipMemset(counters, 0, 2 * sizeof(unsigned long long));
+  const dim3 grid(1u << 23), block(256);  // 2^31 threads per launch
+  for (uint32_t half = 0; err == hipSuccess && half < 2; ++half) {
+    hipLaunchKernelGGL(every_input, grid, block, 0, 0, half << 31, counters);
+    err = hipGetLastError();
+  }
+  const uint32_t highs[] = {0x0000u, 0x0001u, 0x007Fu, 0x0080u, 0x3F80u, 0x4B7Fu,
+                            0x7F7Fu, 0x7F80u, 0x7FC0u, 0x8000u, 0xBF80u, 0xFF7Fu};
+  for (uint32_t hi : highs) {
+    if (err != hipSuccess) break;
+    hipLaunchKernelGGL(every_pair, grid, block, 0, 0, hi, counters);
+    err = hipGetLastError();
+  }
+  if (err == hipSuccess) err = hipDeviceSynchronize();
+  if (err == hipSuccess) {
+    err = hipMemcpy(counters_host, counters, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  }
+  if (counters) (void)hipFree(counters);
+  return static_cast<int>(err);
+}

@@ -1,0 +1,34 @@
+"""The device BF16 stochastic-rounding encoder equals the reference rule on every input.
+
+The kernels round BF16 states with gfx950's v_cvt_sr_bf16_f32; the reference
+rule (sr_states/_bf16.py:37-74) is restated as sr::bf16_sr_bits, which the
+CPU suite pins against the oracles.  tests/native/bf16_sr_check.hip compares
+the two on the device bit for bit, NaN payloads included: every FP32 input
+at its decision boundaries, 0, 0xFFFF and a hashed random value, and every
+(low half, random value) pair for twelve upper halves.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LIBRARY = Path(__file__).resolve().parent / "native" / "libbf16_sr_check.so"
+
+
+def test_hardware_sr_convert_matches_the_reference_rule_exhaustively(cuda):
+    import torch  # noqa: F401  (load the HIP runtime first)
+
+    assert LIBRARY.exists(), f"{LIBRARY} is not built (tests/native/build_checks.py)"
+    check = ctypes.CDLL(str(LIBRARY))
+    check.sr_check_bf16_sr.restype = ctypes.c_int
+    check.sr_check_bf16_sr.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
+    counters = (ctypes.c_ulonglong * 2)()
+    assert check.sr_check_bf16_sr(counters) == 0
+    mismatches, comparisons = counters[0], counters[1]
+    assert comparisons == 5 * 2**32 + 12 * 2**32
+    assert mismatches == 0
