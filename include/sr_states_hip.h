@@ -56,13 +56,10 @@ enum sr_error {
 
 /* Elements one lane moves per tile.  A tile is block_size * (this many)
  * consecutive elements of one tensor and is processed by one workgroup.
- * An optimizer launch whose widest operand is 4 bytes and narrowest is 2
- * bytes (FP32 parameters with 16-bit states) uses SR_LANE_ELEMENTS: FP32
- * operands move as one 128-bit access per lane.  Every other optimizer
- * launch (a one-byte FP8 state, or only 16-bit operands), and every cast,
- * uses SR_LANE_ELEMENTS_NARROW, so that each lane moves at least 8 bytes of
- * every operand.  sr_lane_elements() returns the width of an optimizer
- * launch. */
+ * Optimizer launches currently all use SR_LANE_ELEMENTS (FP32 operands move
+ * as one 128-bit access per lane) and casts SR_LANE_ELEMENTS_NARROW.
+ * sr_lane_elements() returns the width of an optimizer launch; hosts must
+ * use it rather than assume a width. */
 #define SR_LANE_ELEMENTS 4
 #define SR_LANE_ELEMENTS_NARROW 8
 

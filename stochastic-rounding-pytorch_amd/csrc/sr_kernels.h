@@ -3,13 +3,12 @@
 // Work decomposition.  Every launch covers a range of tiles; a tile is
 // blockDim.x * E consecutive elements of one tensor and is processed by
 // exactly one workgroup (no persistent loop).  A lane owns E consecutive
-// elements.  E = 4 when the widest operand is FP32 and none is narrower than
-// 16 bits: FP32 operands move as one 128-bit access per lane, 16-bit states
-// as one 64-bit access.  Every other launch uses E = 8, so that no lane
-// access is narrower than 64 bits.  Measured on MI355X: E4M3 + BF16 moments
-// 5.27 -> 5.50 TB/s at E = 8; BF16 parameters and moments 4.61 -> 4.99 TB/s;
-// BF16 SGDM 4.96 -> 5.76 TB/s; FP32 parameters with 16-bit states are
-// faster at E = 4 (5.67 vs 5.40 TB/s).  Rows whose pointers are not all 16-byte
+// elements.  Optimizer launches use E = 4 (FP32 operands move as one 128-bit
+// access per lane), casts E = 8.  Measured on MI355X with the non-temporal
+// accesses below, E = 4 is the faster optimizer width for every combination
+// tried (E4M3 + BF16 moments 6.03 vs 5.41 TB/s at E = 8, BF16 parameters
+// and momentum 6.47 vs 6.21) and E = 8 the faster cast width (BF16 output
+// 6.08 vs 5.81 TB/s).  Rows whose pointers are not all 16-byte
 // aligned, and the partial last tile of a row, take a coalesced scalar path
 // (element k*blockDim.x + lane of the tile).
 //
@@ -34,16 +33,12 @@
 
 namespace sr {
 
-// Elements per lane of a launch whose operands have encodings p, g, a, b
-// (the host's sr_lane_elements() applies the same rule to dtypes).
-constexpr int lane_elements(int p, int g, int a, int b) {
-  const int w[4] = {enc_bytes(p), enc_bytes(g), enc_bytes(a), enc_bytes(b)};
-  int lo = w[0], hi = w[0];
-  for (int k = 1; k < 4; ++k) {
-    lo = w[k] < lo ? w[k] : lo;
-    hi = w[k] > hi ? w[k] : hi;
-  }
-  return (hi == 4 && lo >= 2) ? SR_LANE_ELEMENTS : SR_LANE_ELEMENTS_NARROW;
+// Elements per lane of an optimizer launch whose operands have encodings
+// p, g, a, b (the host's sr_lane_elements() applies the same rule to dtypes).
+// Every combination currently uses SR_LANE_ELEMENTS; the operands stay part
+// of the contract so that a combination can move without an ABI change.
+constexpr int lane_elements(int /*p*/, int /*g*/, int /*a*/, int /*b*/) {
+  return SR_LANE_ELEMENTS;
 }
 static_assert(SR_LANE_ELEMENTS == 4 && SR_LANE_ELEMENTS_NARROW == 8, "lanes move 4 or 8 elements");
 constexpr int kMaxBlock = 1024;
@@ -104,41 +99,57 @@ __device__ __forceinline__ SR_GLOBAL T* gptr_mut(void* p) {
   return (SR_GLOBAL T*)(p);
 }
 
+// Streaming accesses.  Every operand is read once and written at most once
+// per launch, so every global load and store carries the non-temporal hint.
+// Measured on MI355X: north star 5.64 -> 6.13 TB/s, SGDM 5.87 -> 6.41 TB/s;
+// the hint on loads alone is slower (5.51) and on stores alone neutral.
+typedef uint32_t stream_v4 __attribute__((ext_vector_type(4)));
+typedef uint32_t stream_v2 __attribute__((ext_vector_type(2)));
+
+template <class T>
+__device__ __forceinline__ T stream_load(const void* p) {
+  return __builtin_nontemporal_load(gptr<T>(p));
+}
+template <class T>
+__device__ __forceinline__ void stream_store(void* p, T v) {
+  __builtin_nontemporal_store(v, gptr_mut<T>(p));
+}
+
 // E elements at index i (i a multiple of E, base 16-byte aligned), moved as
 // one access of E * width bytes (two for 32 bytes).
 template <int BYTES>
 __device__ __forceinline__ void load_words(const char* ptr, uint32_t* w) {
   if constexpr (BYTES == 32) {
-    const uint4 a = *gptr<uint4>(ptr), b = *gptr<uint4>(ptr + 16);
+    const stream_v4 a = stream_load<stream_v4>(ptr), b = stream_load<stream_v4>(ptr + 16);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
   } else if constexpr (BYTES == 16) {
-    const uint4 a = *gptr<uint4>(ptr);
+    const stream_v4 a = stream_load<stream_v4>(ptr);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
   } else if constexpr (BYTES == 8) {
-    const uint2 a = *gptr<uint2>(ptr);
+    const stream_v2 a = stream_load<stream_v2>(ptr);
     w[0] = a.x; w[1] = a.y;
   } else if constexpr (BYTES == 4) {
-    w[0] = *gptr<uint32_t>(ptr);
+    w[0] = stream_load<uint32_t>(ptr);
   } else {
     static_assert(BYTES == 2, "unsupported access width");
-    w[0] = *gptr<uint16_t>(ptr);
+    w[0] = stream_load<uint16_t>(ptr);
   }
 }
 
 template <int BYTES>
 __device__ __forceinline__ void store_words(char* ptr, const uint32_t* w) {
   if constexpr (BYTES == 32) {
-    *gptr_mut<uint4>(ptr) = make_uint4(w[0], w[1], w[2], w[3]);
-    *gptr_mut<uint4>(ptr + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+    stream_store(ptr, stream_v4{w[0], w[1], w[2], w[3]});
+    stream_store(ptr + 16, stream_v4{w[4], w[5], w[6], w[7]});
   } else if constexpr (BYTES == 16) {
-    *gptr_mut<uint4>(ptr) = make_uint4(w[0], w[1], w[2], w[3]);
+    stream_store(ptr, stream_v4{w[0], w[1], w[2], w[3]});
   } else if constexpr (BYTES == 8) {
-    *gptr_mut<uint2>(ptr) = make_uint2(w[0], w[1]);
+    stream_store(ptr, stream_v2{w[0], w[1]});
   } else if constexpr (BYTES == 4) {
-    *gptr_mut<uint32_t>(ptr) = w[0];
+    stream_store(ptr, w[0]);
   } else {
     static_assert(BYTES == 2, "unsupported access width");
-    *gptr_mut<uint16_t>(ptr) = static_cast<uint16_t>(w[0]);
+    stream_store(ptr, static_cast<uint16_t>(w[0]));
   }
 }
 
@@ -164,17 +175,19 @@ __device__ __forceinline__ void store_vec(void* base, int64_t i, const uint32_t 
 template <int ENC>
 __device__ __forceinline__ uint32_t load1(const void* base, int64_t i) {
   constexpr int W = enc_bytes(ENC);
-  if constexpr (W == 4) return gptr<uint32_t>(base)[i];
-  else if constexpr (W == 2) return gptr<uint16_t>(base)[i];
-  else return gptr<uint8_t>(base)[i];
+  const char* p = static_cast<const char*>(base) + i * W;
+  if constexpr (W == 4) return stream_load<uint32_t>(p);
+  else if constexpr (W == 2) return stream_load<uint16_t>(p);
+  else return stream_load<uint8_t>(p);
 }
 
 template <int ENC>
 __device__ __forceinline__ void store1(void* base, int64_t i, uint32_t v) {
   constexpr int W = enc_bytes(ENC);
-  if constexpr (W == 4) gptr_mut<uint32_t>(base)[i] = v;
-  else if constexpr (W == 2) gptr_mut<uint16_t>(base)[i] = static_cast<uint16_t>(v);
-  else gptr_mut<uint8_t>(base)[i] = static_cast<uint8_t>(v);
+  char* p = static_cast<char*>(base) + i * W;
+  if constexpr (W == 4) stream_store(p, v);
+  else if constexpr (W == 2) stream_store(p, static_cast<uint16_t>(v));
+  else stream_store(p, static_cast<uint8_t>(v));
 }
 
 // The row record of this workgroup's tile, read once with uniform loads.
@@ -333,7 +346,7 @@ __global__ __launch_bounds__(kMaxBlock) void sgdm_kernel(const SgdmArgs a) {
 // ---------------------------------------------------------------------------
 // Casts move 8 elements per lane whatever the output width: with one load
 // and one store per lane the workgroup count matters more than the access
-// width (BF16 output of 2^24 values: 4.73 TB/s at 4 elements, 5.30 at 8).
+// width (BF16 output of 2^24 values: 5.20 TB/s at 4 elements, 5.41 at 8).
 constexpr int kCastLaneElements = SR_LANE_ELEMENTS_NARROW;
 
 template <int ENC>

@@ -88,8 +88,8 @@ def test_call_raises_with_the_library_message():
         _lib.call("sr_cast", None, None, 16, 9, 0, 0, 0, 256, None)
 
 
-def test_lane_width_follows_operand_widths():
-    """4 elements per lane when the widest operand is 4 bytes and none is under 2; else 8."""
+def test_lane_width_of_every_optimizer_launch():
+    """Every dtype combination currently moves SR_LANE_ELEMENTS per lane; unknown dtypes give 0."""
     import itertools
 
     import torch
@@ -97,15 +97,9 @@ def test_lane_width_follows_operand_widths():
     from sr_states import _lib
 
     lib = _lib.library()
-    widths = {_lib.SR_F32: 4, _lib.SR_BF16: 2, _lib.SR_F16: 2, _lib.SR_E4M3: 1, _lib.SR_E5M2: 1}
+    states = (_lib.SR_F32, _lib.SR_BF16, _lib.SR_F16, _lib.SR_E4M3, _lib.SR_E5M2)
     for p, g in itertools.product((_lib.SR_F32, _lib.SR_BF16), repeat=2):
-        for a, b in itertools.product(widths, repeat=2):
-            w = [widths[d] for d in (p, g, a, b)]
-            expected = _lib.LANE_ELEMENTS if max(w) == 4 and min(w) >= 2 else _lib.LANE_ELEMENTS_NARROW
-            assert lib.sr_lane_elements(p, g, a, b) == expected, (p, g, a, b)
+        for a, b in itertools.product(states, repeat=2):
+            assert lib.sr_lane_elements(p, g, a, b) == _lib.LANE_ELEMENTS, (p, g, a, b)
     assert lib.sr_lane_elements(0, 0, 5, 0) == 0 and lib.sr_lane_elements(-1, 0, 0, 0) == 0
-    f32, bf16, e4m3 = torch.float32, torch.bfloat16, torch.float8_e4m3fn
-    assert _lib.lane_elements(f32, f32, bf16, bf16) == 4  # the north star
-    assert _lib.lane_elements(f32, f32, e4m3, bf16) == 8
-    assert _lib.lane_elements(bf16, bf16, bf16, bf16) == 8
-    assert _lib.lane_elements(f32, f32, f32, f32) == 4
+    assert _lib.lane_elements(torch.float32, torch.float32, torch.float8_e4m3fn, torch.bfloat16) == 4

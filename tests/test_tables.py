@@ -333,11 +333,12 @@ def test_library_is_the_only_execution_path(monkeypatch):
 
 
 def test_buckets_are_tiled_at_their_lane_width(recorder):
-    """FP8 states or all-16-bit operands: 8 elements per lane; FP32 with 16-bit states: 4."""
+    """Tile tables follow the library's lane width for each bucket's dtypes."""
     n, block = 5000, 256
     fp8 = {"exp_avg": StateFormat(torch.float8_e4m3fn), "exp_avg_sq": StateFormat(torch.bfloat16)}
-    cases = [(torch.float32, fp8, _lib.LANE_ELEMENTS_NARROW), (torch.bfloat16, None, _lib.LANE_ELEMENTS_NARROW),
-             (torch.float32, None, _lib.LANE_ELEMENTS)]
+    cases = [(torch.float32, fp8, _lib.lane_elements(torch.float32, torch.float32, torch.float8_e4m3fn, torch.bfloat16)),
+             (torch.bfloat16, None, _lib.lane_elements(*(torch.bfloat16,) * 4)),
+             (torch.float32, None, _lib.lane_elements(torch.float32, torch.float32, torch.bfloat16, torch.bfloat16))]
     for dtype, formats, _ in cases:
         p = torch.nn.Parameter(torch.ones(n, dtype=dtype))
         p.grad = torch.ones_like(p)
