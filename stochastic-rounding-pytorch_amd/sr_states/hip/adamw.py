@@ -19,7 +19,7 @@ from ..optim.adamw import adamw_hparams, validate_adamw
 from ..rounding import native_codes
 from ._common import validate_device, validate_update_device
 from ._multi_tensor import prepare_group, upload
-from ._optimizer import nonnegative, validate_options, validate_tensors
+from ._optimizer import DEFAULT_BLOCK_SIZE, nonnegative, validate_options, validate_tensors
 
 
 def _launch(tables, dtypes, hparams, seed, rng_step, block_size, stream, row_scalars=None):
@@ -69,7 +69,7 @@ def hip_adamw_step_(
     offset: int = 0,
     rounding: str | None = None,
     formats: tuple | dict | None = None,
-    block_size: int = 256,
+    block_size: int = DEFAULT_BLOCK_SIZE,
 ) -> None:
     """Update parameter and moments in place (triton/adamw.py:160-221).
 
@@ -143,7 +143,7 @@ class AdamWHip(StateOptimizer):
         state_dtype=None,
         rounding=None,
         seed=0,
-        block_size=256,
+        block_size=DEFAULT_BLOCK_SIZE,
     ):
         super().__init__(
             params,

@@ -17,7 +17,7 @@ from ..optim.sgd import sgdm_hparams, validate_sgdm
 from ..rounding import native_codes
 from ._common import validate_device, validate_update_device
 from ._multi_tensor import prepare_group
-from ._optimizer import nonnegative, validate_options, validate_tensors
+from ._optimizer import DEFAULT_BLOCK_SIZE, nonnegative, validate_options, validate_tensors
 
 
 def _launch(tables, dtypes, hparams, seed, rng_step, block_size, stream):
@@ -49,7 +49,7 @@ def hip_sgdm_step_(
     offset: int = 0,
     rounding: str | None = None,
     formats: tuple | dict | None = None,
-    block_size: int = 256,
+    block_size: int = DEFAULT_BLOCK_SIZE,
 ) -> None:
     """Apply one fused momentum-SGD update in place (triton/sgd.py:434-490).
 
@@ -116,7 +116,7 @@ class SGDMHip(StateOptimizer):
         state_dtype=None,
         rounding=None,
         seed=0,
-        block_size=256,
+        block_size=DEFAULT_BLOCK_SIZE,
     ):
         super().__init__(
             params,

@@ -23,6 +23,7 @@ import torch
 from conftest import assert_bits_or_nan, ulp_distance
 
 from oracle import sr_oracle
+from sr_states.hip._optimizer import DEFAULT_BLOCK_SIZE
 
 pytestmark = pytest.mark.gpu
 
@@ -213,7 +214,7 @@ def test_one_launch_per_bucket_and_no_launch_on_validation_error(cuda, kind, mon
         return launch(tables, *args)
 
     monkeypatch.setattr(module, "_launch", count)
-    tile = 256 * sr_states._lib.LANE_ELEMENTS  # BF16 moments
+    tile = DEFAULT_BLOCK_SIZE * sr_states._lib.LANE_ELEMENTS  # BF16 moments
 
     def parameter(n, dtype=torch.float32):
         p = torch.nn.Parameter(torch.ones(n, device=cuda, dtype=dtype))

@@ -21,6 +21,7 @@ import sr_states
 from sr_states import AdamWHip, SGDMHip, StateFormat
 from sr_states import _lib
 from sr_states.hip._multi_tensor import GroupTableCache, bucket_items, build_records, build_tile_rows
+from sr_states.hip._optimizer import DEFAULT_BLOCK_SIZE
 from sr_states.optim._state import StateOptimizer, _validate_rng_numel
 
 from oracle import sr_oracle
@@ -243,7 +244,7 @@ def test_launch_scalars_are_the_eager_fp32_roundings(recorder):
 
 def test_one_table_per_bucket_and_no_launch_on_validation_error(recorder):
     """tests/test_triton_multi_tensor.py:184-228 on CPU."""
-    tile = 256 * _lib.LANE_ELEMENTS  # BF16 moments
+    tile = DEFAULT_BLOCK_SIZE * _lib.LANE_ELEMENTS  # BF16 moments
 
     def parameter(n, dtype=torch.float32):
         p = torch.nn.Parameter(torch.ones(n, dtype=dtype))
