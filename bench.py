@@ -18,6 +18,12 @@ read+write, at their storage widths (20 B for FP32 p/g and BF16 moments).
 each step on the launch stream (one launch per step).  ``traffic`` comes
 from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE measurement of the same
 workload, scaled by a copy-kernel calibration, when present.
+``pattern_ceiling`` is the rate of a trivial-math kernel that moves exactly
+the same streams (widths, tile shape and order, non-temporal accesses) over
+the same number of elements (tests/native/stream_ceiling.hip), timed in the
+same process after the workload's tensors are freed: what the memory system
+gives this access pattern at this footprint.  ``frac`` there is the fused
+kernel's rate over it.
 
 cpu_baseline: the reference's eager CPU path (restated in oracle/sr_oracle.py
 with the same torch operations) timed on this host on a bounded sample of
@@ -306,6 +312,37 @@ def cpu_baseline(spec, target_seconds: float = 12.0):
     }
 
 
+CEILING_LIBRARY = ROOT / "tests" / "native" / "libstream_ceiling.so"
+
+
+def pattern_ceiling(spec, elements: int, reps: int):
+    """Rate of the trivial kernel with this workload's streams, or None where none applies.
+
+    Covers FP32-parameter AdamW and SGDM launches whose gradient and states
+    match one of the probe's patterns (tests/native/stream_ceiling.hip).
+    """
+    if spec["optimizer"] not in ("adamw", "sgdm") or spec["p_dtype"] != torch.float32:
+        return None
+    if not CEILING_LIBRARY.exists():
+        return None
+    size = lambda dt: torch.empty((), dtype=dt).element_size()  # noqa: E731
+    widths = [size(spec["g_dtype"])] + [size(dt) for dt, _ in spec["formats"]]
+    if len(widths) == 2:
+        widths.append(0)
+    import ctypes
+
+    lib = ctypes.CDLL(str(CEILING_LIBRARY))
+    lib.sr_stream_ceiling.restype = ctypes.c_int
+    lib.sr_stream_ceiling.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
+    n = elements // 512 * 512
+    ms = ctypes.c_float()
+    if lib.sr_stream_ceiling(n, *widths, reps, ctypes.byref(ms)) != 0:
+        return None
+    return {"achieved": bytes_per_element(spec) * n / ms.value / 1e6, "kernel_ms": ms.value,
+            "elements": n, "kernel": "stream_ceiling.hip: same streams, trivial arithmetic"}
+
+
 def load_traffic(workload: str):
     """HBM bytes per launch from the committed rocprofv3 FETCH/WRITE summary, or None."""
     for path in sorted((ROOT / "profiles").glob(f"*_{workload}_hbm_traffic.md")):
@@ -322,6 +359,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=25)
     parser.add_argument("--workload", choices=sorted(WORKLOADS), default="north_star")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-ceiling", action="store_true",
+                        help="skip the access-pattern ceiling measurement")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     args = parser.parse_args()
     if args.gpus != 1:
@@ -403,9 +442,14 @@ def main():
         },
         "cpu_baseline": None,
     }
+    del params, step
+    torch.cuda.empty_cache()
+    if not args.no_ceiling:
+        ceiling = pattern_ceiling(spec, elements, reps=max(5, min(50, int(300 / kernel_ms))))
+        if ceiling is not None:
+            ceiling["frac"] = achieved / ceiling["achieved"]
+        result["roofline"]["pattern_ceiling"] = ceiling
     if not args.no_cpu_baseline and spec["optimizer"] != "copy":
-        del params, step
-        torch.cuda.empty_cache()
         result["cpu_baseline"] = cpu_baseline(spec, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 

@@ -166,7 +166,10 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n,
  * Row r spans ceil(numel / T) tiles of T = block_size *
  * sr_lane_elements(p_dtype, g_dtype, m_dtype, v_dtype) elements.  The
  * tables live in device memory and are not checked: tables that break these
- * rules make the kernel access memory out of bounds.
+ * rules make the kernel access memory out of bounds.  total_tiles may be up
+ * to 2^31 - 4096 (SR_ERR_ARGUMENT beyond); launches whose grid would carry
+ * 2^32 or more work-items in one dimension are split into rows of
+ * workgroups, so one call covers buckets past 2^34 elements.
  * Keys are derived on the device from (seed, rng_step, param_index).
  * Replaces `_multi_adamw_kernel` and its launch
  * (sr_states/triton/adamw.py:102-157, 289-319). */

@@ -78,13 +78,15 @@ int param_enc(int index) { return index == 0 ? sr::ENC_F32 : sr::ENC_BF16_RN; }
 bool valid_block(int block) { return block >= 64 && block <= sr::kMaxBlock && block % 64 == 0; }
 
 // One workgroup per tile; the grid is padded to a whole number of XCD chunk
-// rounds so that the kernels' tile order (sr_tile_order.h) is a permutation.
-// `tiles` must equal the total_tiles the kernel argument carries.
+// rounds so that the kernels' tile order (sr_tile_order.h) is a permutation,
+// and split into rows when one dimension would carry 2^32 or more
+// work-items (2^34 elements at four per lane).  `tiles` must equal the
+// total_tiles the kernel argument carries.
 int launch(const void* fn, int block, uint32_t tiles, void* arg, void* stream) {
-  const uint64_t grid = sr::padded_grid(tiles);
-  if (grid > 0x7FFFFFFFull) return fail(SR_ERR_ARGUMENT, "%u tiles exceed the grid limit", tiles);
+  if (sr::padded_grid(tiles) > 0x7FFFFFFFull) return fail(SR_ERR_ARGUMENT, "%u tiles exceed the grid limit", tiles);
+  const sr::LaunchShape shape = sr::launch_shape(tiles, static_cast<uint32_t>(block));
   void* args[] = {arg};
-  hipError_t err = hipLaunchKernel(fn, dim3(static_cast<unsigned>(grid)), dim3(block), args, 0,
+  hipError_t err = hipLaunchKernel(fn, dim3(shape.x, shape.y), dim3(block), args, 0,
                                    static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return hip_fail(err, "hipLaunchKernel");
   return SR_OK;

@@ -74,9 +74,11 @@ struct CastArgs {
 };
 
 // Logical tile of this workgroup; >= total_tiles for the padding workgroups.
-// The host launches padded_grid(total_tiles) workgroups.
+// The host launches launch_shape(total_tiles, block): one row of
+// padded_grid(total_tiles) workgroups, or several rows when that many would
+// exceed the dispatch packet's 32-bit work-item count.
 __device__ __forceinline__ uint32_t logical_tile(uint32_t total_tiles) {
-  return tile_of(blockIdx.x, total_tiles);
+  return tile_of(blockIdx.y * gridDim.x + blockIdx.x, total_tiles);
 }
 
 // ---------------------------------------------------------------------------

@@ -42,11 +42,35 @@ SR_HOST_DEVICE inline uint64_t padded_grid(uint32_t tiles) {
   return (static_cast<uint64_t>(tiles) + unit - 1) / unit * unit;
 }
 
-// Tile of workgroup b < padded_grid(tiles); values >= tiles mark padding.
+// Tile of workgroup b; values >= tiles mark padding.  The result is
+// b - x + x * 2^s - 7 * (k mod 2^s), within 7 * 2^s of b, so it does not wrap
+// for b < 2^32 - 3584; every b at or past padded_grid(tiles) maps to padding.
 SR_HOST_DEVICE inline uint32_t tile_of(uint32_t b, uint32_t tiles) {
   const uint32_t s = chunk_shift(tiles);
   const uint32_t k = b / kXcds, x = b % kXcds;
   return (((k >> s) * kXcds + x) << s) | (k & ((1u << s) - 1u));
+}
+
+// A dispatch packet holds the grid size in work-items as a 32-bit number per
+// dimension, so one dimension carries fewer than 2^32 work-items (HIP
+// rejects larger launches).  Launches whose padded grid exceeds that are
+// laid out as `y` rows of `x` workgroups; x is a whole number of chunk
+// rounds (a multiple of 8 << chunk_shift), so workgroup b = y_index * x +
+// x_index still runs on XCD b mod 8 and the tile order above is unchanged.
+// Workgroups past padded_grid(tiles) map to padding.  `max_items` is the
+// per-dimension work-item limit; tests pass smaller values.
+struct LaunchShape {
+  uint32_t x, y;
+};
+
+SR_HOST_DEVICE inline LaunchShape launch_shape(uint32_t tiles, uint32_t block,
+                                               uint64_t max_items = 0xFFFFFFFFull) {
+  const uint64_t grid = padded_grid(tiles);
+  if (grid * block <= max_items) return {static_cast<uint32_t>(grid), 1u};
+  const uint64_t unit = static_cast<uint64_t>(kXcds) << chunk_shift(tiles);
+  uint64_t per_row = max_items / block / unit * unit;
+  if (per_row == 0) per_row = unit;  // only for limits below one chunk round
+  return {static_cast<uint32_t>(per_row), static_cast<uint32_t>((grid + per_row - 1) / per_row)};
 }
 
 }  // namespace sr

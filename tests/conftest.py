@@ -25,8 +25,8 @@ def pytest_configure(config):
     # Markers are registered in pytest.ini.
     built = (PACKAGE_DIR / "sr_states").glob("_group_walk*.so")
     library = PACKAGE_DIR / "sr_states" / "libsr_states_hip.so"
-    check = ROOT / "tests" / "native" / "libbf16_sr_check.so"
-    if not check.exists() and not torch.cuda.is_available():
+    checks = [ROOT / "tests" / "native" / name for name in ("libbf16_sr_check.so", "libstream_ceiling.so")]
+    if not all(check.exists() for check in checks) and not torch.cuda.is_available():
         import importlib.util
 
         spec = importlib.util.spec_from_file_location("sr_checks", ROOT / "tests" / "native" / "build_checks.py")

@@ -1,9 +1,15 @@
 """Compile the device-side checks under tests/native for gfx950.
 
-``build()`` writes tests/native/libbf16_sr_check.so (the exhaustive BF16
-stochastic-rounding check of bf16_sr_check.hip) with the library's own HIP
-flags.  __graft_entry__.build() calls it; tests/conftest.py calls it on a
-CPU checkout where it is missing.  GPU runs use the prebuilt file.
+``build()`` writes, with the library's own HIP flags:
+
+- tests/native/libbf16_sr_check.so, the exhaustive BF16 stochastic-rounding
+  check of bf16_sr_check.hip;
+- tests/native/libstream_ceiling.so, the trivial-math kernel of
+  stream_ceiling.hip that measures the bandwidth ceiling of the fused
+  update's access pattern (bench.py and tests/test_gpu_stream_ceiling.py).
+
+__graft_entry__.build() calls it; tests/conftest.py calls it on a CPU
+checkout where a library is missing.  GPU runs use the prebuilt files.
 """
 
 from __future__ import annotations
@@ -16,6 +22,8 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parents[1]
 CHECK_LIBRARY = HERE / "libbf16_sr_check.so"
+CEILING_LIBRARY = HERE / "libstream_ceiling.so"
+LIBRARIES = {CHECK_LIBRARY: HERE / "bf16_sr_check.hip", CEILING_LIBRARY: HERE / "stream_ceiling.hip"}
 
 
 def _package_build():
@@ -27,15 +35,16 @@ def _package_build():
     return module
 
 
-def build() -> Path:
+def build() -> list[Path]:
     package = _package_build()
-    tmp = CHECK_LIBRARY.with_name(CHECK_LIBRARY.name + ".tmp")
-    cmd = [package.HIPCC, *package.HIP_FLAGS, "-shared", str(HERE / "bf16_sr_check.hip"), "-o", str(tmp)]
-    result = subprocess.run(cmd, capture_output=True, text=True)
-    if result.returncode != 0:
-        raise RuntimeError(f"command failed ({result.returncode}): {' '.join(cmd)}\n{result.stderr}")
-    os.replace(tmp, CHECK_LIBRARY)
-    return CHECK_LIBRARY
+    for library, source in LIBRARIES.items():
+        tmp = library.with_name(library.name + ".tmp")
+        cmd = [package.HIPCC, *package.HIP_FLAGS, "-shared", str(source), "-o", str(tmp)]
+        result = subprocess.run(cmd, capture_output=True, text=True)
+        if result.returncode != 0:
+            raise RuntimeError(f"command failed ({result.returncode}): {' '.join(cmd)}\n{result.stderr}")
+        os.replace(tmp, library)
+    return list(LIBRARIES)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,139 @@
+// The bandwidth ceiling of a fused update's access pattern, measured.
+//
+// A kernel with trivial arithmetic (XORs) that moves exactly the
+// streams of one fused-update launch: an FP32 parameter read and written, a
+// gradient read, and one or two states read and written, with the product's
+// tile shape (128 lanes x 4 elements), its XCD-chunked tile order
+// (sr_tile_order.h) and its non-temporal accesses.  Whatever rate this
+// kernel reaches for n elements is what the memory system gives that access
+// pattern at that footprint; the fused kernels do strictly more work per
+// byte, so their rate over this one says how much of the reachable
+// bandwidth their arithmetic and table lookups cost.
+//
+// Measurement helper only: bench.py reports it beside the fused kernel's
+// rate and tests/test_gpu_stream_ceiling.py checks the fused kernels against
+// it.  It allocates its own buffers, so it never touches caller memory.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../stochastic-rounding-pytorch_amd/csrc/sr_tile_order.h"
+
+namespace {
+
+constexpr int kBlock = 128;
+constexpr int kLanes = 4;
+constexpr uint32_t kTile = kBlock * kLanes;
+
+typedef uint32_t word4 __attribute__((ext_vector_type(4)));
+typedef uint32_t word2 __attribute__((ext_vector_type(2)));
+
+// The access type of kLanes elements of `BYTES` bytes each.
+template <int BYTES> struct Access;
+template <> struct Access<4> { typedef word4 type; };
+template <> struct Access<2> { typedef word2 type; };
+template <> struct Access<1> { typedef uint32_t type; };
+
+// Every word of every load feeds a value that every stored word depends on,
+// so the compiler can neither drop nor narrow an access.
+__device__ __forceinline__ uint32_t fold(const word4& w) { return w.x ^ w.y ^ w.z ^ w.w; }
+__device__ __forceinline__ uint32_t fold(const word2& w) { return w.x ^ w.y; }
+__device__ __forceinline__ uint32_t fold(uint32_t w) { return w; }
+
+template <int BYTES>
+__device__ __forceinline__ typename Access<BYTES>::type load(const void* base, uint64_t i) {
+  return __builtin_nontemporal_load(
+      reinterpret_cast<const typename Access<BYTES>::type*>(static_cast<const char*>(base) + i * BYTES));
+}
+template <int BYTES>
+__device__ __forceinline__ void store(void* base, uint64_t i, typename Access<BYTES>::type w) {
+  __builtin_nontemporal_store(
+      w, reinterpret_cast<typename Access<BYTES>::type*>(static_cast<char*>(base) + i * BYTES));
+}
+
+// G, M, V: bytes per element of the gradient and the two states (V = 0: one
+// state).  Tile t covers elements [t * kTile, (t + 1) * kTile) < n.
+template <int G, int M, int V>
+__global__ __launch_bounds__(kBlock) void streams(void* p, const void* g, void* m, void* v, uint32_t tiles) {
+  const uint32_t t = sr::tile_of(blockIdx.y * gridDim.x + blockIdx.x, tiles);
+  if (t >= tiles) return;
+  const uint64_t i = static_cast<uint64_t>(t) * kTile + threadIdx.x * kLanes;
+  // Every load is issued before any store, as in the fused kernels: the
+  // pointers may alias as far as the compiler knows, so a load placed after
+  // a store would wait for it.
+  auto wp = load<4>(p, i);
+  auto wg = load<G>(g, i);
+  auto wm = load<M>(m, i);
+  typename Access<(V > 0 ? V : 1)>::type wv{};
+  if constexpr (V > 0) wv = load<V>(v, i);
+  const uint32_t h = fold(wg) ^ fold(wp) ^ fold(wm) ^ fold(wv);
+  wp ^= h;
+  wm ^= h;
+  wv ^= h;
+  store<4>(p, i, wp);
+  store<M>(m, i, wm);
+  if constexpr (V > 0) store<V>(v, i, wv);
+}
+
+typedef void (*Kernel)(void*, const void*, void*, void*, uint32_t);
+
+Kernel pick(int g, int m, int v) {
+  if (g == 4 && m == 2 && v == 2) return streams<4, 2, 2>;
+  if (g == 2 && m == 2 && v == 2) return streams<2, 2, 2>;
+  if (g == 4 && m == 1 && v == 2) return streams<4, 1, 2>;
+  if (g == 4 && m == 2 && v == 0) return streams<4, 2, 0>;
+  return nullptr;
+}
+
+}  // namespace
+
+// Average milliseconds per launch of the trivial kernel over n elements with
+// a gradient of g_bytes and states of m_bytes and v_bytes per element
+// (v_bytes 0: one state), over `reps` launches after two untimed ones.
+// Supported patterns: (4,2,2), (2,2,2), (4,1,2), (4,2,0).  n must be a
+// positive multiple of 512 with n / 512 <= 2^31 - 4096 (the fused
+// launches' tile limit); the grid is laid out as the fused launches lay it
+// out (sr::launch_shape).  Returns 0, or 1 for an
+// unsupported argument, 2 for a HIP error (buffers are freed either way).
+extern "C" int sr_stream_ceiling(uint64_t n, int g_bytes, int m_bytes, int v_bytes, int reps,
+                                 float* avg_ms) {
+  const Kernel kernel = pick(g_bytes, m_bytes, v_bytes);
+  if (!kernel || n == 0 || n % kTile || n / kTile > 0x7FFFF000ull || reps < 1 || !avg_ms) return 1;
+  const uint32_t tiles = static_cast<uint32_t>(n / kTile);
+  const sr::LaunchShape shape = sr::launch_shape(tiles, kBlock);
+  const size_t bytes[4] = {n * 4, n * g_bytes, n * m_bytes, n * v_bytes};
+  void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t start = nullptr, stop = nullptr;
+  int rc = 2;
+  do {
+    if (hipDeviceSynchronize() != hipSuccess) break;
+    bool ok = true;
+    for (int k = 0; k < 4 && ok; ++k) {
+      if (bytes[k] == 0) continue;
+      ok = hipMalloc(&buf[k], bytes[k]) == hipSuccess && hipMemset(buf[k], 0x3A, bytes[k]) == hipSuccess;
+    }
+    if (!ok) break;
+    if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess) break;
+    auto launch = [&] {
+      hipLaunchKernelGGL(kernel, dim3(shape.x, shape.y), dim3(kBlock), 0, nullptr, buf[0], buf[1], buf[2], buf[3],
+                         tiles);
+    };
+    launch();
+    launch();
+    if (hipGetLastError() != hipSuccess || hipEventRecord(start, nullptr) != hipSuccess) break;
+    for (int r = 0; r < reps; ++r) launch();
+    if (hipGetLastError() != hipSuccess || hipEventRecord(stop, nullptr) != hipSuccess ||
+        hipEventSynchronize(stop) != hipSuccess)
+      break;
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, start, stop) != hipSuccess) break;
+    *avg_ms = ms / reps;
+    rc = 0;
+  } while (false);
+  if (start) (void)hipEventDestroy(start);
+  if (stop) (void)hipEventDestroy(stop);
+  (void)hipDeviceSynchronize();
+  for (void* b : buf)
+    if (b) (void)hipFree(b);
+  return rc;
+}

@@ -2,7 +2,10 @@
 // the host: for every launch size tried, the workgroups of padded_grid(tiles)
 // cover each tile in [0, tiles) exactly once, padding stays below one eighth
 // of the grid (or one chunk round for small launches), and each XCD's
-// workgroups walk whole chunks of 2^chunk_shift consecutive tiles.
+// workgroups walk whole chunks of 2^chunk_shift consecutive tiles.  It also
+// checks launch_shape: one row when the padded grid fits the per-dimension
+// work-item limit, otherwise rows of whole chunk rounds whose workgroups,
+// numbered row by row, still cover each tile exactly once.
 #include <cstdint>
 #include <cstdio>
 #include <vector>
@@ -33,6 +36,36 @@ int check(uint32_t tiles) {
   return 0;
 }
 
+// launch_shape under a per-dimension limit of `max_items` work-items.
+int check_shape(uint32_t tiles, uint32_t block, uint64_t max_items, bool walk) {
+  const sr::LaunchShape shape = sr::launch_shape(tiles, block, max_items);
+  const uint64_t grid = sr::padded_grid(tiles);
+  const uint64_t unit = static_cast<uint64_t>(sr::kXcds) << sr::chunk_shift(tiles);
+  const uint64_t total = static_cast<uint64_t>(shape.x) * shape.y;
+  if (grid * block <= max_items) return shape.x == grid && shape.y == 1 ? 0 : 11;
+  if (static_cast<uint64_t>(shape.x) * block > max_items && shape.x != unit) return 12;
+  if (shape.x % unit != 0 || shape.y < 2 || total < grid || total - grid >= shape.x) return 13;
+  if (total + 3584 >= (1ull << 32)) return 14;
+  if (!walk) {
+    // Only the workgroups past the padded grid: all padding, none wrapped.
+    for (uint64_t b = grid; b < total; ++b) {
+      const uint32_t t = sr::tile_of(static_cast<uint32_t>(b), tiles);
+      if (t < tiles || t + 3584ull < b) return 15;
+    }
+    return 0;
+  }
+  std::vector<uint8_t> seen(tiles, 0);
+  for (uint64_t b = 0; b < total; ++b) {
+    const uint32_t t = sr::tile_of(static_cast<uint32_t>(b), tiles);
+    if (b >= grid && t < tiles) return 16;
+    if (t < tiles && seen[t]++) return 17;
+  }
+  for (uint32_t t = 0; t < tiles; ++t) {
+    if (!seen[t]) return 18;
+  }
+  return 0;
+}
+
 int main() {
   int failures = 0;
   std::vector<uint32_t> sizes;
@@ -51,6 +84,32 @@ int main() {
     std::printf("chunk_shift breakpoints moved\n");
     ++failures;
   }
-  std::printf("%zu launch sizes, %d failures\n", sizes.size(), failures);
+  int shapes = 0;
+  for (uint32_t tiles : {1u, 63u, 64u, 4095u, 4096u, 4097u, 32769u, 121524u, 1000003u}) {
+    for (uint32_t block : {64u, 128u, 256u, 1024u}) {
+      for (uint64_t limit : {1ull << 16, 1ull << 20, (1ull << 24) + 4096 * 64, 0xFFFFFFFFull}) {
+        ++shapes;
+        if (int rc = check_shape(tiles, block, limit, true)) {
+          std::printf("tiles %u block %u limit %llu: failure %d\n", tiles, block, (unsigned long long)limit, rc);
+          ++failures;
+        }
+      }
+    }
+  }
+  // At the real limit: 2^34 + 2^20 elements in 512-element tiles (two rows),
+  // and the largest tile count a launch accepts.
+  struct Big { uint32_t tiles, block; bool walk; };
+  for (const Big& big : {Big{33556480u, 128u, true}, Big{0x7FFFF000u, 1024u, false}, Big{0x7FFFF000u, 64u, false}}) {
+    ++shapes;
+    const sr::LaunchShape shape = sr::launch_shape(big.tiles, big.block);
+    if (shape.y < 2) {
+      std::printf("tiles %u block %u: expected several rows\n", big.tiles, big.block);
+      ++failures;
+    } else if (int rc = check_shape(big.tiles, big.block, 0xFFFFFFFFull, big.walk)) {
+      std::printf("tiles %u block %u: failure %d\n", big.tiles, big.block, rc);
+      ++failures;
+    }
+  }
+  std::printf("%zu launch sizes, %d launch shapes, %d failures\n", sizes.size(), shapes, failures);
   return failures != 0;
 }
