@@ -150,6 +150,42 @@ def test_builtin_casts_never_run_on_the_cpu():
         sr_states.sr_cast_bf16(x, seed=1)
 
 
+@pytest.mark.parametrize("arch", ["gfx950:sramecc+:xnack-", "gfx950", "gfx942:sramecc+:xnack-", "gfx90a", "gfx1100"])
+def test_device_check_accepts_only_the_built_architecture(monkeypatch, arch):
+    """tests/test_fp8_storage.py:88-108, with the gfx950 check in place of sm_89.
+
+    The library holds gfx950 code only, so every dtype (FP8 included) runs on
+    gfx950 and nothing runs elsewhere; the architecture is queried once per
+    device and CPU tensors are refused before any query.
+    """
+    from sr_states.hip import _common
+
+    _common._device_arch.cache_clear()
+    seen = []
+
+    class Properties:
+        gcnArchName = arch
+
+    def properties(device):
+        seen.append(torch.device(device))
+        return Properties()
+
+    monkeypatch.setattr(torch.cuda, "get_device_properties", properties)
+    try:
+        for _ in range(2):
+            if arch.split(":")[0] == "gfx950":
+                _common.validate_update_device(torch.device("cuda", 0), torch.float8_e4m3fn, torch.float8_e5m2)
+                _common.validate_device("cuda:0")
+            else:
+                with pytest.raises(ValueError, match=f"built for gfx950, not {arch.split(':')[0]}"):
+                    _common.validate_update_device(torch.device("cuda", 0), torch.float8_e4m3fn)
+        with pytest.raises(ValueError, match="GPU tensors"):
+            _common.validate_device(torch.device("cpu"))
+        assert seen == [torch.device("cuda", 0)]
+    finally:
+        _common._device_arch.cache_clear()
+
+
 @pytest.mark.parametrize("cls", CLASSES)
 def test_hip_optimizers_reject_reference_only_rules(cls):
     """tests/test_rounding_registry.py:86-90."""
