@@ -90,6 +90,30 @@ def test_stream_partition_invariance(cuda, dtype):
     assert_bits_or_nan(parts, whole)
 
 
+@pytest.mark.parametrize("dtype,ulp", [(torch.bfloat16, 2.0**-7), (torch.float16, 2.0**-10),
+                                       (torch.float8_e4m3fn, 2.0**-3), (torch.float8_e5m2, 2.0**-2)])
+def test_seed_reproducibility_and_counter_periodicity(cuda, dtype, ulp):
+    """tests/test_seed_reproducibility.py:6-36 on the device, per stochastic format.
+
+    The same seed and offset reproduce the output; another seed changes the
+    choices of inexact values; seed and offset act modulo 2^32, for negative
+    and very large Python integers too.
+    """
+    import sr_states
+
+    x = torch.linspace(-10, 10, 10003, device=cuda)
+    first = sr_states.cast(x, dtype=dtype, seed=1234, offset=77)
+    assert_bits_or_nan(sr_states.cast(x, dtype=dtype, seed=1234, offset=77), first)
+    inexact = torch.full((4096,), 1.0 + ulp / 4, device=cuda)
+    assert not torch.equal(sr_states.cast(inexact, dtype=dtype, seed=1).float(),
+                           sr_states.cast(inexact, dtype=dtype, seed=2).float())
+    y = torch.linspace(-1, 1, 1003, device=cuda)
+    expected = sr_states.cast(y, dtype=dtype, seed=7, offset=31)
+    for periods in (-(2**60), -1, 1, 2**60):
+        actual = sr_states.cast(y, dtype=dtype, seed=7 + periods * 2**32, offset=31 + periods * 2**32)
+        assert_bits_or_nan(actual, expected, f"{periods} periods")
+
+
 def test_unaligned_noncontiguous_and_empty_inputs(cuda):
     import sr_states
 

@@ -162,6 +162,34 @@ def test_adamw_zero_gradient_and_decay(cuda, betas):
     assert torch.count_nonzero(m) == 0 and torch.count_nonzero(v) == 0
 
 
+def test_round_to_nearest_variants_store_deterministic_bf16_state(cuda):
+    """tests/test_reference_optimizers.py:90-104 on the device.
+
+    The RN classes store BF16 states rounded to nearest even: the first
+    momentum equals the gradient converted by torch, and neither class's
+    states depend on the seed.
+    """
+    import sr_states
+
+    runs = []
+    for seed in (0, 12345):
+        q = torch.nn.Parameter(torch.linspace(-1, 1, 1027, device=cuda))
+        q.grad = torch.cos(q.detach())
+        sgd = sr_states.SGDMHipRN([q], lr=0.01, seed=seed)
+        sgd.step()
+        assert torch.equal(sgd.state[q]["momentum_buffer"], q.grad.float().to(torch.bfloat16))
+        p = torch.nn.Parameter(torch.linspace(-1, 1, 1027, device=cuda))
+        p.grad = torch.sin(p.detach())
+        adam = sr_states.AdamWHipRN([p], lr=0.01, seed=seed)
+        adam.step()
+        adam.step()
+        states = [adam.state[p][name] for name in ("exp_avg", "exp_avg_sq")]
+        assert all(s.dtype == torch.bfloat16 for s in states)
+        runs.append((p.detach().clone(), *states))
+    for a, b in zip(*runs):
+        assert_bits_or_nan(a, b)
+
+
 @pytest.mark.parametrize("kind", ["adamw", "sgdm"])
 def test_validation_and_disjoint_buffers(cuda, kind):
     """tests/test_triton_states.py:213-234."""
