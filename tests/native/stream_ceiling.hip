@@ -10,6 +10,9 @@
 // byte, so their rate over this one says how much of the reachable
 // bandwidth their arithmetic and table lookups cost.
 //
+// sr_cast_ceiling does the same for the cast's pattern (FP32 in, a 2- or
+// 1-byte format out) with the cast's launch shape.
+//
 // Measurement helper only: bench.py reports it beside the fused kernel's
 // rate and tests/test_gpu_stream_ceiling.py checks the fused kernels against
 // it.  It allocates its own buffers, so it never touches caller memory.
@@ -75,6 +78,30 @@ __global__ __launch_bounds__(kBlock) void streams(void* p, const void* g, void* 
   if constexpr (V > 0) store<V>(v, i, wv);
 }
 
+// The cast's pattern: 8 FP32 elements read and 8 narrower ones written per
+// lane (OUT = 2 or 1 bytes), in workgroups of kCastBlock lanes as the cast
+// kernel launches them.  Every output word takes bits of every input word.
+constexpr int kCastBlock = 256;
+constexpr int kCastLanes = 8;
+constexpr uint32_t kCastTile = kCastBlock * kCastLanes;
+
+template <int OUT>
+__global__ __launch_bounds__(kCastBlock) void cast_streams(const void* x, void* y, uint32_t tiles) {
+  const uint32_t t = sr::tile_of(blockIdx.y * gridDim.x + blockIdx.x, tiles);
+  if (t >= tiles) return;
+  const uint64_t i = static_cast<uint64_t>(t) * kCastTile + threadIdx.x * kCastLanes;
+  const word4 a = load<4>(x, i), b = load<4>(x, i + kLanes);
+  if constexpr (OUT == 2) {
+    const word4 out = {(a.x >> 16) | (a.y & 0xFFFF0000u), (a.z >> 16) | (a.w & 0xFFFF0000u),
+                       (b.x >> 16) | (b.y & 0xFFFF0000u), (b.z >> 16) | (b.w & 0xFFFF0000u)};
+    __builtin_nontemporal_store(out, reinterpret_cast<word4*>(static_cast<char*>(y) + i * 2));
+  } else {
+    const word2 out = {(a.x >> 24) | ((a.y >> 16) & 0xFF00u) | ((a.z >> 8) & 0xFF0000u) | (a.w & 0xFF000000u),
+                       (b.x >> 24) | ((b.y >> 16) & 0xFF00u) | ((b.z >> 8) & 0xFF0000u) | (b.w & 0xFF000000u)};
+    __builtin_nontemporal_store(out, reinterpret_cast<word2*>(static_cast<char*>(y) + i));
+  }
+}
+
 typedef void (*Kernel)(void*, const void*, void*, void*, uint32_t);
 
 Kernel pick(int g, int m, int v) {
@@ -135,5 +162,58 @@ extern "C" int sr_stream_ceiling(uint64_t n, int g_bytes, int m_bytes, int v_byt
   (void)hipDeviceSynchronize();
   for (void* b : buf)
     if (b) (void)hipFree(b);
+  return rc;
+}
+
+// Average milliseconds per launch of the cast-pattern kernel over n FP32
+// elements written as out_bytes-wide ones (2 or 1), rotating through
+// `buffers` input/output pairs (1-16) so that a pair is reused only after
+// the others have passed through the caches, over `reps` launches after
+// one untimed round.  n must be a positive multiple of 2048 with
+// n / 2048 <= 2^31 - 4096.  Returns 0, 1 for an unsupported argument, or 2
+// for a HIP error (buffers are freed either way).
+extern "C" int sr_cast_ceiling(uint64_t n, int out_bytes, int buffers, int reps, float* avg_ms) {
+  if ((out_bytes != 1 && out_bytes != 2) || buffers < 1 || buffers > 16 || n == 0 || n % kCastTile ||
+      n / kCastTile > 0x7FFFF000ull || reps < 1 || !avg_ms)
+    return 1;
+  const uint32_t tiles = static_cast<uint32_t>(n / kCastTile);
+  const sr::LaunchShape shape = sr::launch_shape(tiles, kCastBlock);
+  void (*kernel)(const void*, void*, uint32_t) = out_bytes == 2 ? cast_streams<2> : cast_streams<1>;
+  void* in[16] = {};
+  void* out[16] = {};
+  hipEvent_t start = nullptr, stop = nullptr;
+  int rc = 2;
+  do {
+    if (hipDeviceSynchronize() != hipSuccess) break;
+    bool ok = true;
+    for (int k = 0; k < buffers && ok; ++k) {
+      ok = hipMalloc(&in[k], n * 4) == hipSuccess && hipMemset(in[k], 0x3A, n * 4) == hipSuccess &&
+           hipMalloc(&out[k], n * out_bytes) == hipSuccess;
+    }
+    if (!ok) break;
+    if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess) break;
+    int turn = 0;
+    auto launch = [&] {
+      hipLaunchKernelGGL(kernel, dim3(shape.x, shape.y), dim3(kCastBlock), 0, nullptr, in[turn], out[turn], tiles);
+      turn = (turn + 1) % buffers;
+    };
+    for (int k = 0; k < buffers; ++k) launch();
+    if (hipGetLastError() != hipSuccess || hipEventRecord(start, nullptr) != hipSuccess) break;
+    for (int r = 0; r < reps; ++r) launch();
+    if (hipGetLastError() != hipSuccess || hipEventRecord(stop, nullptr) != hipSuccess ||
+        hipEventSynchronize(stop) != hipSuccess)
+      break;
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, start, stop) != hipSuccess) break;
+    *avg_ms = ms / reps;
+    rc = 0;
+  } while (false);
+  if (start) (void)hipEventDestroy(start);
+  if (stop) (void)hipEventDestroy(stop);
+  (void)hipDeviceSynchronize();
+  for (int k = 0; k < 16; ++k) {
+    if (in[k]) (void)hipFree(in[k]);
+    if (out[k]) (void)hipFree(out[k]);
+  }
   return rc;
 }

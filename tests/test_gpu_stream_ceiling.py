@@ -1,4 +1,4 @@
-"""The fused kernels against the bandwidth ceiling of their own access pattern.
+"""The fused kernels and the cast against the bandwidth ceiling of their own access pattern.
 
 tests/native/stream_ceiling.hip moves exactly the streams of a fused launch
 (same element widths, tile shape, tile order and non-temporal accesses) with
@@ -72,3 +72,45 @@ def test_fused_kernel_reaches_the_ceiling_of_its_access_pattern(cuda, kind):
     assert fused_ms <= ceiling_ms / 0.93, (
         f"{kind}: fused {rate(fused_ms):.0f} GB/s against the pattern's ceiling {rate(ceiling_ms):.0f} GB/s")
     assert torch.isfinite(p).all()
+
+
+def test_cast_reaches_the_ceiling_of_its_access_pattern(cuda):
+    """The SR cast at config 1's size (2^24 elements) over eight rotating buffer pairs."""
+    import sr_states
+    from sr_states.hip.cast import native_cast
+
+    n, pairs = 1 << 24, 8
+    assert LIBRARY.exists(), f"{LIBRARY} is not built (tests/native/build_checks.py)"
+    lib = ctypes.CDLL(str(LIBRARY))
+    lib.sr_cast_ceiling.restype = ctypes.c_int
+    lib.sr_cast_ceiling.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.POINTER(ctypes.c_float)]
+    gen = torch.Generator(device=cuda).manual_seed(1)
+    inputs = [torch.empty(n, device=cuda).normal_(generator=gen) for _ in range(pairs)]
+    outputs = [torch.empty(n, device=cuda, dtype=torch.bfloat16) for _ in range(pairs)]
+    turn = [0]
+
+    def step():
+        k = turn[0] = (turn[0] + 1) % pairs
+        native_cast(inputs[k], dtype=torch.bfloat16, rule=sr_states._lib.SR_STOCHASTIC, seed=7, out=outputs[k])
+
+    reps = 1000
+    fused, ceiling = [], []
+    for _ in range(3):
+        ms = ctypes.c_float()
+        assert lib.sr_cast_ceiling(n, 2, pairs, reps, ctypes.byref(ms)) == 0
+        ceiling.append(ms.value)
+        for _ in range(pairs):
+            step()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            step()
+        stop.record()
+        stop.synchronize()
+        fused.append(start.elapsed_time(stop) / reps)
+    fused_ms, ceiling_ms = statistics.median(fused), statistics.median(ceiling)
+    rate = lambda ms: 6 * n / ms / 1e6  # noqa: E731  (GB/s)
+    assert fused_ms <= ceiling_ms / 0.93, (
+        f"cast: {rate(fused_ms):.0f} GB/s against the pattern's ceiling {rate(ceiling_ms):.0f} GB/s")
