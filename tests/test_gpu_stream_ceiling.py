@@ -5,9 +5,11 @@ tests/native/stream_ceiling.hip moves exactly the streams of a fused launch
 trivial arithmetic, so its rate for n elements is what the memory system
 gives that pattern at that footprint.  The fused AdamW (BF16-SR moments) and
 momentum SGD (FP16-SR momentum) on one FP32 parameter of n elements move the
-same bytes and must reach at least 93% of that rate, measured interleaved in
-one process.  On MI355X they reach 99-100% of it: the hashing, rounding and
-table lookups are hidden under the memory traffic.
+same bytes and must reach at least 90% of that rate, measured interleaved in
+one process.  On MI355X they reach 98-103% of it: the hashing, rounding and
+table lookups are hidden under the memory traffic.  The bound leaves room
+for the 2-4% by which either rate moves with where fresh allocations land
+physically.
 """
 
 from __future__ import annotations
@@ -69,7 +71,7 @@ def test_fused_kernel_reaches_the_ceiling_of_its_access_pattern(cuda, kind):
         fused.append(_fused_ms(opt.step))
     fused_ms, ceiling_ms = statistics.median(fused), statistics.median(ceiling)
     rate = lambda ms: bytes_per_element * N / ms / 1e6  # noqa: E731  (GB/s)
-    assert fused_ms <= ceiling_ms / 0.93, (
+    assert fused_ms <= ceiling_ms / 0.90, (
         f"{kind}: fused {rate(fused_ms):.0f} GB/s against the pattern's ceiling {rate(ceiling_ms):.0f} GB/s")
     assert torch.isfinite(p).all()
 
@@ -112,5 +114,5 @@ def test_cast_reaches_the_ceiling_of_its_access_pattern(cuda):
         fused.append(start.elapsed_time(stop) / reps)
     fused_ms, ceiling_ms = statistics.median(fused), statistics.median(ceiling)
     rate = lambda ms: 6 * n / ms / 1e6  # noqa: E731  (GB/s)
-    assert fused_ms <= ceiling_ms / 0.93, (
+    assert fused_ms <= ceiling_ms / 0.90, (
         f"cast: {rate(fused_ms):.0f} GB/s against the pattern's ceiling {rate(ceiling_ms):.0f} GB/s")
