@@ -15,9 +15,12 @@ Roofline: the kernel is HBM-bound.  Algorithmic bytes per element are the
 minimum reads+writes: parameter read+write, gradient read, each moment
 read+write, at their storage widths (20 B for FP32 p/g and BF16 moments).
 ``achieved`` = bytes per launch / mean kernel time: two HIP events on the
-launch stream bracket the K back-to-back steps (one launch per step).  ``traffic`` comes
-from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE measurement of the same
-workload, scaled by a copy-kernel calibration, when present.
+launch stream bracket the K back-to-back steps (one launch per step).  A
+second pass of K steps, each between its own two events, gives
+``step_ms_median`` (and min, max); those events add about 2 us per step.
+``traffic`` comes from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+measurement of the same workload, scaled by a copy-kernel calibration, when
+present.
 ``pattern_ceiling`` is the rate of a trivial-math kernel that moves exactly
 the same streams (widths, tile shape and order, non-temporal accesses) over
 the same number of elements (tests/native/stream_ceiling.hip), timed in the
@@ -403,6 +406,16 @@ def main():
     # duration.  No events sit between the steps: on an 18 us cast they would
     # add about 2 us each.
     kernel_ms = ms_per_step
+    # Spread of single steps: a second pass of K steps, each between its own
+    # two events (which add about 2 us per step on the launch stream).
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    for i in range(args.steps):
+        starts[i].record()
+        step()
+        ends[i].record()
+    torch.cuda.synchronize()
+    step_ms = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
 
     bpe = bytes_per_element(spec)
     bytes_per_launch = bpe * elements
@@ -446,6 +459,9 @@ def main():
             "frac": achieved / HBM_PEAK_GBPS,
             "traffic": traffic,
             "kernel_ms": kernel_ms,
+            "step_ms_median": step_ms[len(step_ms) // 2],
+            "step_ms_min": step_ms[0],
+            "step_ms_max": step_ms[-1],
             "algorithmic_bytes_per_launch": bytes_per_launch,
         },
         "cpu_baseline": None,
