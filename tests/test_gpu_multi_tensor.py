@@ -145,9 +145,10 @@ def test_multi_tensor_matches_functional_updates_byte_for_byte(cuda, kind, dtype
 
 
 def _golden_cases():
-    if not GOLDEN.exists():
-        return []
-    return list(torch.load(GOLDEN, weights_only=True)["cases"].items())
+    # A missing fixture is a collection error, not zero cases.
+    cases = list(torch.load(GOLDEN, weights_only=True)["cases"].items())
+    assert len(cases) == 3, [name for name, _ in cases]
+    return cases
 
 
 @pytest.mark.parametrize("name,case", _golden_cases(), ids=lambda v: v if isinstance(v, str) else "")
