@@ -128,6 +128,11 @@ SR_HD uint32_t bf16_sr_bits(uint32_t b, uint32_t hash) {
 SR_HD uint32_t bf16_sr(uint32_t b, uint32_t hash) {
 #if defined(__HIP_DEVICE_COMPILE__)
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  // An empty asm hides the hash from the optimizer (it emits nothing).
+  // Otherwise LLVM folds the shift below through the hash's last xor-shift
+  // into its second multiply: y*C << 16 becomes y*(C << 16), one more
+  // quarter-rate v_mul_lo_u32 per element where a shift would do.
+  __asm__("" : "+v"(hash));
   const bf16x2 out =
       __builtin_amdgcn_cvt_sr_bf16_f32(bf16x2{}, __builtin_bit_cast(float, b), hash << 16, false);
   return __builtin_bit_cast(uint32_t, out) & 0xFFFFu;
