@@ -2,8 +2,10 @@
 //
 // Everything here is a pure function of its arguments, usable on the host
 // (key derivation, CPU-side unit checks) and on gfx950.  Encoders work on the
-// IEEE-754 bit patterns with integer ALU only, so they need no FP mode
-// assumptions.  The FP32 recurrences use explicit fmaf() exactly where the
+// IEEE-754 bit patterns with integer ALU, except that the device finishes
+// BF16 stochastic rounding with gfx950's stochastic convert and the minifloat
+// encodings with a hardware convert of an exactly representable value; both
+// are checked exhaustively against the integer forms on the device.  The FP32 recurrences use explicit fmaf() exactly where the
 // reference's eager CPU kernels fuse, and must be compiled with
 // -ffp-contract=off so that no other multiply-add is contracted.
 #pragma once
@@ -214,6 +216,74 @@ SR_HD uint32_t minifloat_bits(uint32_t b, uint32_t hash) {
   return enc | sign;
 }
 
+// Convert of an FP32 value that F represents exactly (for FP16 also values
+// of magnitude 65536 and up, which IEEE rounding takes to Inf): one
+// hardware convert on the device, the integer nearest form on the host.
+template <class F>
+SR_HD uint32_t exact_convert(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  if constexpr (F::kWidth == 16) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+  } else if constexpr (F::kM == 3) {
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false)) & 0xFFu;
+  } else {
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(v, 0.0f, 0, false)) & 0xFFu;
+  }
+#else
+  return minifloat_bits<F, false>(f32_bits(v), 0u);
+#endif
+}
+
+// minifloat_bits on the device, bit for bit, with fewer instructions.  With
+// D = s the number of dropped significand bits, the stochastic rule "round
+// up iff (hash >> 8) < rem * 2^(24-D)" equals "iff T < rem" for
+// T = (hash >> 8) >> (24 - D), and for D <= 23 the dropped bits are the low
+// D bits of the FP32 pattern, so the rounded value's FP32 bits are
+//   (a + (2^D - 1 - T)) & ~(2^D - 1)         (stochastic)
+//   (a + 2^(D-1) - 1 + lsb) & ~(2^D - 1)     (nearest even)
+// with the carry into the exponent doing what q + up does in the integer
+// form.  lsb is q's parity: bit D of the significand, which for D = 23 is
+// the implicit bit (q = 1), not the exponent bit stored there.  For D >= 24 the result is 0 or the smallest subnormal, decided as
+// in minifloat_bits.  The value is then exactly representable (or, for
+// FP16, at least 65536 and taken to Inf), so a hardware convert finishes
+// the encoding.  tests/native/minifloat_check.hip compares the two on every
+// FP32 input: for nearest with no random value, for stochastic at the
+// random values where each input's decision flips and at the extremes.
+template <class F, bool STOCH>
+SR_HD uint32_t minifloat_bits_fast(uint32_t b, uint32_t hash) {
+  const uint32_t sign = b & 0x80000000u;
+  uint32_t a = b & 0x7FFFFFFFu;
+  const bool nan = a > 0x7F800000u;
+  if (F::kSat) a = a < F::kMaxBits ? a : F::kMaxBits;  // also maps +-Inf to +-max
+  const int E = static_cast<int>(a >> 23);
+  const int below = F::kEmin + 127 - (E ? E : 1);  // binades below the smallest normal
+  const int D = 23 - F::kM + (below > 0 ? below : 0);
+  uint32_t r;
+  if (D <= 23) {
+    const uint32_t mask = (1u << D) - 1u;
+    const uint32_t add = STOCH ? mask - ((hash >> 8) >> (24 - D)) : (mask >> 1) + (((a | 0x00800000u) >> D) & 1u);
+    r = (a + add) & ~mask;
+  } else {
+    const uint32_t sig = E ? ((a & 0x007FFFFFu) | 0x00800000u) : a;
+    const int t = D - 24;
+    const bool up = STOCH ? (t < 24 && (hash >> 8) < (sig >> t)) : (t == 0 && sig > 0x00800000u);
+    r = up ? static_cast<uint32_t>(F::kEmin - F::kM + 127) << 23 : 0u;  // 2^(EMIN-M) or 0
+  }
+  const uint32_t enc = exact_convert<F>(bits_f32(r | sign));
+  return nan ? (F::kNan | (sign >> (32 - F::kWidth))) : enc;
+}
+
+// The minifloat encoders: the integer form on the host, its bit-exact
+// hardware-finished form on the device.
+template <class F, bool STOCH>
+SR_HD uint32_t minifloat_encode(uint32_t b, uint32_t hash) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return minifloat_bits_fast<F, STOCH>(b, hash);
+#else
+  return minifloat_bits<F, STOCH>(b, hash);
+#endif
+}
+
 // Encode an FP32 value into the storage bits of `ENC` with the counter's
 // hash.  The hash is only evaluated for stochastic encodings.
 template <int ENC>
@@ -226,18 +296,18 @@ SR_HD uint32_t encode(float x, uint32_t counter) {
   } else if constexpr (ENC == ENC_BF16_SR) {
     return bf16_sr(b, h32(counter));
   } else if constexpr (ENC == ENC_F16_RN) {
-    return minifloat_bits<F16, false>(b, 0);
+    return minifloat_encode<F16, false>(b, 0);
   } else if constexpr (ENC == ENC_F16_SR) {
-    return minifloat_bits<F16, true>(b, h32(counter));
+    return minifloat_encode<F16, true>(b, h32(counter));
   } else if constexpr (ENC == ENC_E4M3_RN) {
-    return minifloat_bits<E4M3, false>(b, 0);
+    return minifloat_encode<E4M3, false>(b, 0);
   } else if constexpr (ENC == ENC_E4M3_SR) {
-    return minifloat_bits<E4M3, true>(b, h32(counter));
+    return minifloat_encode<E4M3, true>(b, h32(counter));
   } else if constexpr (ENC == ENC_E5M2_RN) {
-    return minifloat_bits<E5M2, false>(b, 0);
+    return minifloat_encode<E5M2, false>(b, 0);
   } else {
     static_assert(ENC == ENC_E5M2_SR, "unknown encoding");
-    return minifloat_bits<E5M2, true>(b, h32(counter));
+    return minifloat_encode<E5M2, true>(b, h32(counter));
   }
 }
 
@@ -262,6 +332,25 @@ SR_HD float minifloat_value(uint32_t v) {
   return bits_f32(sign | ((E - 1u + (uint32_t)(127 + F::kEmin)) << 23) | (man << (23 - F::kM)));
 }
 
+// minifloat_value on the device with one hardware convert: equal for every
+// encoding that is not a NaN, and a NaN for every NaN encoding (payloads are
+// not part of the contract), checked for every encoding by
+// tests/native/minifloat_check.hip.
+template <class F>
+SR_HD float minifloat_decode(uint32_t v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  if constexpr (F::kWidth == 16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v)));
+  } else if constexpr (F::kM == 3) {
+    return __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(v), 0);
+  } else {
+    return __builtin_amdgcn_cvt_f32_bf8(static_cast<int>(v), 0);
+  }
+#else
+  return minifloat_value<F>(v);
+#endif
+}
+
 // Decode storage bits of `ENC` to the exact FP32 value.
 template <int ENC>
 SR_HD float decode(uint32_t v) {
@@ -270,11 +359,11 @@ SR_HD float decode(uint32_t v) {
   } else if constexpr (ENC == ENC_BF16_RN || ENC == ENC_BF16_SR) {
     return bits_f32(v << 16);
   } else if constexpr (ENC == ENC_F16_RN || ENC == ENC_F16_SR) {
-    return minifloat_value<F16>(v);
+    return minifloat_decode<F16>(v);
   } else if constexpr (ENC == ENC_E4M3_RN || ENC == ENC_E4M3_SR) {
-    return minifloat_value<E4M3>(v);
+    return minifloat_decode<E4M3>(v);
   } else {
-    return minifloat_value<E5M2>(v);
+    return minifloat_decode<E5M2>(v);
   }
 }
 

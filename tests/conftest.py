@@ -25,7 +25,8 @@ def pytest_configure(config):
     # Markers are registered in pytest.ini.
     built = (PACKAGE_DIR / "sr_states").glob("_group_walk*.so")
     library = PACKAGE_DIR / "sr_states" / "libsr_states_hip.so"
-    checks = [ROOT / "tests" / "native" / name for name in ("libbf16_sr_check.so", "libstream_ceiling.so")]
+    checks = [ROOT / "tests" / "native" / name
+              for name in ("libbf16_sr_check.so", "libstream_ceiling.so", "libminifloat_check.so")]
     if not all(check.exists() for check in checks) and not torch.cuda.is_available():
         import importlib.util
 

@@ -4,6 +4,8 @@
 
 - tests/native/libbf16_sr_check.so, the exhaustive BF16 stochastic-rounding
   check of bf16_sr_check.hip;
+- tests/native/libminifloat_check.so, the exhaustive check of the device
+  minifloat encoders of minifloat_check.hip;
 - tests/native/libstream_ceiling.so, the trivial-math kernel of
   stream_ceiling.hip that measures the bandwidth ceiling of the fused
   update's access pattern (bench.py and tests/test_gpu_stream_ceiling.py).
@@ -23,7 +25,9 @@ HERE = Path(__file__).resolve().parent
 ROOT = HERE.parents[1]
 CHECK_LIBRARY = HERE / "libbf16_sr_check.so"
 CEILING_LIBRARY = HERE / "libstream_ceiling.so"
-LIBRARIES = {CHECK_LIBRARY: HERE / "bf16_sr_check.hip", CEILING_LIBRARY: HERE / "stream_ceiling.hip"}
+MINIFLOAT_LIBRARY = HERE / "libminifloat_check.so"
+LIBRARIES = {CHECK_LIBRARY: HERE / "bf16_sr_check.hip", CEILING_LIBRARY: HERE / "stream_ceiling.hip",
+             MINIFLOAT_LIBRARY: HERE / "minifloat_check.hip"}
 
 
 def _package_build():

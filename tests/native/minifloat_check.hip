@@ -1,0 +1,114 @@
+// Exhaustive device check of the minifloat encoders and decoders: the
+// device paths sr::minifloat_bits_fast (bit arithmetic finished by a
+// hardware convert) and sr::minifloat_decode (one hardware convert) against
+// the integer forms sr::minifloat_bits and sr::minifloat_value, for FP16,
+// E4M3 and E5M2.
+//   decode:     every encoding; equal bits, or NaN for NaN;
+//   nearest:    every FP32 input;
+//   stochastic: every FP32 input with six random values: the two values
+//               where its rounding decision flips (threshold - 1 and
+//               threshold, in the upper 24 bits, with low bytes 0xFF and
+//               0x00), 0, 0xFFFFFFFF and a hashed value.  Both forms round
+//               up exactly when (random >> 8) is below a threshold of the
+//               input, so agreement at the flip and the extremes is
+//               agreement for every random value.
+// Built by __graft_entry__.build() into tests/native/libminifloat_check.so and
+// run by tests/test_gpu_minifloat_check.py.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../stochastic-rounding-pytorch_amd/csrc/sr_math.h"
+
+namespace {
+
+__device__ unsigned long long wave_sum(unsigned long long x) {
+  for (int offset = 32; offset > 0; offset >>= 1) x += __shfl_xor(x, offset, 64);
+  return x;
+}
+
+__device__ void add(unsigned long long* counters, unsigned long long mismatches,
+                    unsigned long long checks) {
+  const unsigned long long m = wave_sum(mismatches), c = wave_sum(checks);
+  if ((threadIdx.x & 63) == 0) {
+    if (m) atomicAdd(&counters[0], m);
+    atomicAdd(&counters[1], c);
+  }
+}
+
+// The 24-bit threshold of input b: the integer form rounds up iff
+// (hash >> 8) < threshold (its s <= 24 and s > 24 branches).
+template <class F>
+__device__ uint32_t threshold(uint32_t b) {
+  uint32_t a = b & 0x7FFFFFFFu;
+  if (F::kSat) a = a < F::kMaxBits ? a : F::kMaxBits;
+  const int E = static_cast<int>(a >> 23);
+  const uint32_t sig = E ? ((a & 0x007FFFFFu) | 0x00800000u) : a;
+  const int e_raw = (E ? E : 1) - 127;
+  const int e = (E - 127) > F::kEmin ? (E - 127) : F::kEmin;
+  const int s = 23 - F::kM + (e - e_raw);
+  if (s <= 24) return (sig & ((1u << s) - 1u)) << (24 - s);
+  const int t = s - 24;
+  return t < 24 ? sig >> t : 0u;
+}
+
+// One launch covers 2^31 inputs starting at `base`.
+template <class F>
+__global__ void every_input(uint32_t base, unsigned long long* counters) {
+  const uint32_t b = base + blockIdx.x * blockDim.x + threadIdx.x;
+  unsigned long long mismatches =
+      sr::minifloat_bits_fast<F, false>(b, 0u) != sr::minifloat_bits<F, false>(b, 0u);
+  const uint32_t th = threshold<F>(b);
+  const uint32_t below = th ? ((th - 1u) << 8) | 0xFFu : 0u;
+  const uint32_t randoms[6] = {below, th << 8, th << 8 | 0xFFu, 0u, 0xFFFFFFFFu, sr::h32(b ^ 0x5bd1e995u)};
+  for (uint32_t r : randoms) {
+    mismatches += sr::minifloat_bits_fast<F, true>(b, r) != sr::minifloat_bits<F, true>(b, r);
+  }
+  add(counters, mismatches, 7);
+}
+
+// Every encoding of F: the hardware decode equals the integer one, or both
+// are NaN.
+template <class F>
+__global__ void every_code(unsigned long long* counters) {
+  const uint32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+  const bool valid = v < (1u << F::kWidth);
+  unsigned long long mismatch = 0;
+  if (valid) {
+    const float want = sr::minifloat_value<F>(v), got = sr::minifloat_decode<F>(v);
+    mismatch = want != want ? !(got != got) : sr::f32_bits(got) != sr::f32_bits(want);
+  }
+  add(counters, mismatch, valid ? 1 : 0);
+}
+
+template <class F>
+hipError_t sweep(unsigned long long* counters) {
+  hipLaunchKernelGGL(every_code<F>, dim3(256), dim3(256), 0, 0, counters);
+  const dim3 grid(1u << 23), block(256);  // 2^31 threads per launch
+  hipError_t err = hipGetLastError();
+  for (uint32_t half = 0; err == hipSuccess && half < 2; ++half) {
+    hipLaunchKernelGGL(every_input<F>, grid, block, 0, 0, half << 31, counters);
+    err = hipGetLastError();
+  }
+  return err;
+}
+
+}  // namespace
+
+// format: 0 FP16, 1 E4M3, 2 E5M2.  counters_host[0] = mismatches,
+// [1] = comparisons.  Returns 0, a hipError_t, or -1 for an unknown format.
+extern "C" int sr_check_minifloat(int format, unsigned long long* counters_host) {
+  if (format < 0 || format > 2) return -1;
+  unsigned long long* counters = nullptr;
+  hipError_t err = hipMalloc(&counters, 2 * sizeof(unsigned long long));
+  if (err == hipSuccess) err = hipMemset(counters, 0, 2 * sizeof(unsigned long long));
+  if (err == hipSuccess) {
+    err = format == 0 ? sweep<sr::F16>(counters) : format == 1 ? sweep<sr::E4M3>(counters) : sweep<sr::E5M2>(counters);
+  }
+  if (err == hipSuccess) err = hipDeviceSynchronize();
+  if (err == hipSuccess) {
+    err = hipMemcpy(counters_host, counters, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  }
+  if (counters) (void)hipFree(counters);
+  return static_cast<int>(err);
+}
