@@ -216,12 +216,18 @@ SR_HD uint32_t minifloat_bits(uint32_t b, uint32_t hash) {
   return enc | sign;
 }
 
-// Convert of an FP32 value that F represents exactly (for FP16 also values
-// of magnitude 65536 and up, which IEEE rounding takes to Inf): one
-// hardware convert on the device, the integer nearest form on the host.
+// FP32 bits -> F rounded to nearest even, with IEEE overflow to Inf for
+// FP16 (the FP8 callers clamp to the format maximum first): one hardware
+// convert on the device, the integer nearest form on the host.  Exact for
+// values F represents.  The empty asm makes the input opaque: otherwise,
+// where the bits are those of an FMA result, the compiler may fuse the FMA
+// and the convert into one mixed-precision instruction that rounds once,
+// straight to F, instead of to FP32 first.
 template <class F>
-SR_HD uint32_t exact_convert(float v) {
+SR_HD uint32_t nearest_convert(uint32_t bits) {
 #if defined(__HIP_DEVICE_COMPILE__)
+  __asm__("" : "+v"(bits));
+  const float v = __builtin_bit_cast(float, bits);
   if constexpr (F::kWidth == 16) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
   } else if constexpr (F::kM == 3) {
@@ -230,46 +236,50 @@ SR_HD uint32_t exact_convert(float v) {
     return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(v, 0.0f, 0, false)) & 0xFFu;
   }
 #else
-  return minifloat_bits<F, false>(f32_bits(v), 0u);
+  return minifloat_bits<F, false>(bits, 0u);
 #endif
 }
 
-// minifloat_bits on the device, bit for bit, with fewer instructions.  With
-// D = s the number of dropped significand bits, the stochastic rule "round
-// up iff (hash >> 8) < rem * 2^(24-D)" equals "iff T < rem" for
+// minifloat_bits on the device, bit for bit, with fewer instructions.
+// Nearest even is the convert's own rounding, applied to the (clamped)
+// input.  Stochastic: with D = s the number of dropped significand bits,
+// "round up iff (hash >> 8) < rem * 2^(24-D)" equals "iff T < rem" for
 // T = (hash >> 8) >> (24 - D), and for D <= 23 the dropped bits are the low
 // D bits of the FP32 pattern, so the rounded value's FP32 bits are
-//   (a + (2^D - 1 - T)) & ~(2^D - 1)         (stochastic)
-//   (a + 2^(D-1) - 1 + lsb) & ~(2^D - 1)     (nearest even)
+//   (a + 2^D - 1 - T) & ~(2^D - 1)
 // with the carry into the exponent doing what q + up does in the integer
-// form.  lsb is q's parity: bit D of the significand, which for D = 23 is
-// the implicit bit (q = 1), not the exponent bit stored there.  For D >= 24 the result is 0 or the smallest subnormal, decided as
-// in minifloat_bits.  The value is then exactly representable (or, for
-// FP16, at least 65536 and taken to Inf), so a hardware convert finishes
-// the encoding.  tests/native/minifloat_check.hip compares the two on every
-// FP32 input: for nearest with no random value, for stochastic at the
-// random values where each input's decision flips and at the extremes.
+// form.  For D >= 24 the result is 0 or the smallest subnormal, decided as
+// in minifloat_bits.  That value is exactly representable (or, for FP16, at
+// least 65536 and taken to Inf), so the convert finishes the encoding
+// exactly.  tests/native/minifloat_check.hip compares the two on every FP32
+// input: nearest once, stochastic at the random values where each input's
+// decision flips and at the extremes.
 template <class F, bool STOCH>
 SR_HD uint32_t minifloat_bits_fast(uint32_t b, uint32_t hash) {
   const uint32_t sign = b & 0x80000000u;
   uint32_t a = b & 0x7FFFFFFFu;
   const bool nan = a > 0x7F800000u;
   if (F::kSat) a = a < F::kMaxBits ? a : F::kMaxBits;  // also maps +-Inf to +-max
+  if constexpr (!STOCH) {
+    // Nearest even on the target grid, with IEEE overflow to Inf for FP16,
+    // is the convert's own rounding; the FP8 formats saturate by the clamp.
+    const uint32_t enc = nearest_convert<F>(a | sign);
+    return nan ? (F::kNan | (sign >> (32 - F::kWidth))) : enc;
+  }
   const int E = static_cast<int>(a >> 23);
   const int below = F::kEmin + 127 - (E ? E : 1);  // binades below the smallest normal
   const int D = 23 - F::kM + (below > 0 ? below : 0);
   uint32_t r;
   if (D <= 23) {
     const uint32_t mask = (1u << D) - 1u;
-    const uint32_t add = STOCH ? mask - ((hash >> 8) >> (24 - D)) : (mask >> 1) + (((a | 0x00800000u) >> D) & 1u);
-    r = (a + add) & ~mask;
+    r = (a + mask - ((hash >> 8) >> (24 - D))) & ~mask;
   } else {
     const uint32_t sig = E ? ((a & 0x007FFFFFu) | 0x00800000u) : a;
     const int t = D - 24;
-    const bool up = STOCH ? (t < 24 && (hash >> 8) < (sig >> t)) : (t == 0 && sig > 0x00800000u);
+    const bool up = t < 24 && (hash >> 8) < (sig >> t);
     r = up ? static_cast<uint32_t>(F::kEmin - F::kM + 127) << 23 : 0u;  // 2^(EMIN-M) or 0
   }
-  const uint32_t enc = exact_convert<F>(bits_f32(r | sign));
+  const uint32_t enc = nearest_convert<F>(r | sign);  // exact: r is on the grid
   return nan ? (F::kNan | (sign >> (32 - F::kWidth))) : enc;
 }
 
