@@ -112,3 +112,4 @@ extern "C" int sr_check_minifloat(int format, unsigned long long* counters_host)
   if (counters) (void)hipFree(counters);
   return static_cast<int>(err);
 }
+
