@@ -112,4 +112,3 @@ extern "C" int sr_check_minifloat(int format, unsigned long long* counters_host)
   if (counters) (void)hipFree(counters);
   return static_cast<int>(err);
 }
-
