@@ -266,15 +266,21 @@ SR_HD uint32_t minifloat_bits_fast(uint32_t b, uint32_t hash) {
     const uint32_t enc = nearest_convert<F>(a | sign);
     return nan ? (F::kNan | (sign >> (32 - F::kWidth))) : enc;
   }
+  // An FP32 subnormal (E = 0) is far below F's smallest subnormal; taking
+  // its exponent as 0 instead of 1 keeps it in the second branch, where it
+  // never rounds up, as in the integer form.  The two branches (and the
+  // t < 24 test) stay real branches: waves whose elements all take one
+  // side skip the other, which measured 3-6% faster on FP8 casts than
+  // computing both sides with selects.
   const int E = static_cast<int>(a >> 23);
-  const int below = F::kEmin + 127 - (E ? E : 1);  // binades below the smallest normal
+  const int below = F::kEmin + 127 - E;  // binades below the smallest normal
   const int D = 23 - F::kM + (below > 0 ? below : 0);
   uint32_t r;
   if (D <= 23) {
     const uint32_t mask = (1u << D) - 1u;
     r = (a + mask - ((hash >> 8) >> (24 - D))) & ~mask;
   } else {
-    const uint32_t sig = E ? ((a & 0x007FFFFFu) | 0x00800000u) : a;
+    const uint32_t sig = (a & 0x007FFFFFu) | 0x00800000u;
     const int t = D - 24;
     const bool up = t < 24 && (hash >> 8) < (sig >> t);
     r = up ? static_cast<uint32_t>(F::kEmin - F::kM + 127) << 23 : 0u;  // 2^(EMIN-M) or 0
