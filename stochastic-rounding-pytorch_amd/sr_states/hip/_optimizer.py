@@ -6,6 +6,7 @@ import math
 
 import torch
 
+from ..optim._dtensor import is_dtensor
 from ..rounding import validate_rounding
 
 # Workgroup sizes (threads).  Results do not depend on the choice.
@@ -63,6 +64,11 @@ def validate_no_overlap(spans):
 
 def validate_tensors(parameter, gradient, *states):
     tensors = (parameter, gradient, *states)
+    if any(is_dtensor(t) for t in tensors):
+        raise TypeError(
+            "fused state updates take local tensors: pass each DTensor's to_local() and the "
+            "flat index of the shard's first element as offset"
+        )
     if parameter.device.type != "cuda":
         raise ValueError("fused state updates require GPU tensors")
     validate_tensor_layout(tensors)

@@ -170,10 +170,7 @@ class AdamWHip(StateOptimizer):
     def _step_parameter(self, parameter, state, group, formats, step, seed, offset):
         beta1, beta2 = group["betas"]
         hip_adamw_step_(
-            parameter,
-            parameter.grad,
-            state["exp_avg"],
-            state["exp_avg_sq"],
+            *self._local_tensors(parameter, state),
             lr=group["lr"],
             beta1=beta1,
             beta2=beta2,

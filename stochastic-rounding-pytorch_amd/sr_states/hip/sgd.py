@@ -136,9 +136,7 @@ class SGDMHip(StateOptimizer):
 
     def _step_parameter(self, parameter, state, group, formats, step, seed, offset):
         hip_sgdm_step_(
-            parameter,
-            parameter.grad,
-            state["momentum_buffer"],
+            *self._local_tensors(parameter, state),
             lr=group["lr"],
             momentum_factor=group["momentum"],
             seed=seed,

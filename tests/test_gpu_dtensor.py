@@ -1,0 +1,164 @@
+"""DTensor parameters on the device: every rank's update is its slice of the unsharded update.
+
+A model's parameters are updated unsharded (plain tensors) and, for every
+rank of several meshes, as DTensors holding that rank's shards.  Each local
+parameter, state and step must equal the matching flat range of the
+unsharded result, bit for bit: the random stream of an element depends only
+on its flat index in the whole parameter (the reference's flat-split
+property, tests/test_rng_streams.py:122-150, which its optimizers cannot use
+with DTensors, sr_states/optim/_state.py:148-152).
+
+Ranks are simulated in one process on cuda:0: each rank's DeviceMesh is
+built with ``_rank`` and no process group, so nothing is communicated; the
+kernels see only the local shards.  Shapes leave uneven and empty shards.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from conftest import assert_bits_or_nan
+
+pytest.importorskip("torch.distributed.tensor")
+from torch.distributed.device_mesh import DeviceMesh  # noqa: E402
+from torch.distributed.tensor import DTensor, Replicate, Shard  # noqa: E402
+
+import sr_states  # noqa: E402
+from sr_states.optim._dtensor import shard_start  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(7, 33), (130,), (5, 3, 17), (1,), (3, 1000), (2051,)]
+MESHES = [
+    ((2,), (Shard(0),)),
+    ((3,), (Shard(0),)),
+    ((4,), (Shard(0),)),
+    ((2, 2), (Shard(0), Shard(0))),
+    ((2, 2), (Replicate(), Shard(0))),
+]
+STEPS = 3
+
+
+def _mesh(shape, rank):
+    # Meshes compare equal whatever rank they were built for, and DTensor
+    # caches sharding decisions by mesh: each simulated rank names its mesh
+    # dimensions apart.
+    ranks = torch.arange(int(np.prod(shape))).reshape(shape)
+    names = tuple(f"rank{rank}_dim{i}" for i in range(len(shape)))
+    return DeviceMesh("cuda", ranks, mesh_dim_names=names, _init_backend=False, _rank=rank)
+
+
+def _shard(full, mesh, placements):
+    """DTensor of ``full`` on ``mesh``: torch.chunk along each sharded dim (FSDP2's split)."""
+    block = full
+    for size, index, placement in zip(mesh.shape, mesh.get_coordinate(), placements):
+        if isinstance(placement, Shard):
+            chunks = torch.chunk(block, size, dim=placement.dim)
+            if index < len(chunks):
+                block = chunks[index]
+            else:
+                empty = list(block.shape)
+                empty[placement.dim] = 0
+                block = block.new_empty(empty)
+    return DTensor.from_local(block.contiguous().clone(), mesh, placements, run_check=False,
+                              shape=full.shape, stride=full.stride())
+
+
+def _problem(cuda, seed):
+    gen = torch.Generator(device=cuda).manual_seed(seed)
+    params = [torch.randn(shape, device=cuda, generator=gen) * 0.02 for shape in SHAPES]
+    grads = [[torch.randn(shape, device=cuda, generator=gen) * 1e-3 for shape in SHAPES]
+             for _ in range(STEPS)]
+    return params, grads
+
+
+def _run(make, params, grads, wrap, checkpoint_after=None):
+    """STEPS steps of ``make(parameters)``; ``wrap`` turns a full tensor into a parameter value."""
+    parameters = [torch.nn.Parameter(wrap(p)) for p in params]
+    optimizer = make(parameters)
+    for step, step_grads in enumerate(grads, start=1):
+        for parameter, g in zip(parameters, step_grads):
+            parameter.grad = wrap(g)
+        optimizer.step()
+        if step == checkpoint_after:
+            saved = optimizer.state_dict()
+            optimizer = make(parameters)
+            optimizer.load_state_dict(saved)
+    return parameters, optimizer
+
+
+def _compare(full_params, full_opt, shard_params, shard_opt, names, what):
+    for index, (full, shard) in enumerate(zip(full_params, shard_params)):
+        start = shard_start(shard)
+        local = shard.to_local().reshape(-1)
+        stop = start + local.numel()
+        label = f"{what}, parameter {index} {tuple(full.shape)}, elements [{start}, {stop})"
+        assert_bits_or_nan(local, full.detach().reshape(-1)[start:stop], f"{label}: parameter")
+        full_state, shard_state = full_opt.state[full], shard_opt.state[shard]
+        for name in names:
+            stored = shard_state[name]
+            assert isinstance(stored, DTensor) and stored.placements == shard.placements
+            assert stored.dtype == full_state[name].dtype
+            assert_bits_or_nan(stored.to_local().reshape(-1), full_state[name].reshape(-1)[start:stop],
+                               f"{label}: {name}")
+        assert shard_state.get("step") == full_state.get("step")
+
+
+def _adamw_bf16_sr(parameters):
+    return sr_states.AdamWHip(parameters, lr=1e-3, weight_decay=0.01, seed=11)
+
+
+def _adamw_e4m3_bf16(parameters):
+    formats = {"exp_avg": sr_states.StateFormat(torch.float8_e4m3fn),
+               "exp_avg_sq": sr_states.StateFormat(torch.bfloat16)}
+    return sr_states.AdamWHip(parameters, lr=1e-3, seed=12, state_format=formats)
+
+
+def _sgdm_fp16_sr(parameters):
+    return sr_states.SGDMHip(parameters, lr=0.1, state_dtype=torch.float16, seed=13)
+
+
+OPTIMIZERS = {
+    "adamw_bf16_sr": (_adamw_bf16_sr, ("exp_avg", "exp_avg_sq")),
+    "adamw_e4m3_bf16": (_adamw_e4m3_bf16, ("exp_avg", "exp_avg_sq")),
+    "sgdm_fp16_sr": (_sgdm_fp16_sr, ("momentum_buffer",)),
+}
+
+
+@pytest.mark.parametrize("mesh_shape, placements", MESHES)
+@pytest.mark.parametrize("kind", list(OPTIMIZERS))
+def test_fused_optimizers_update_each_shard_as_its_slice_of_the_whole(cuda, kind, mesh_shape, placements):
+    make, names = OPTIMIZERS[kind]
+    params, grads = _problem(cuda, seed=len(kind) + len(mesh_shape))
+    full_params, full_opt = _run(make, params, grads, lambda t: t.clone())
+    for rank in range(int(np.prod(mesh_shape))):
+        mesh = _mesh(mesh_shape, rank)
+        shard_params, shard_opt = _run(make, params, grads, lambda t: _shard(t, mesh, placements),
+                                       checkpoint_after=2)
+        torch.cuda.synchronize()
+        _compare(full_params, full_opt, shard_params, shard_opt, names, f"{kind} rank {rank}")
+
+
+def test_per_parameter_path_updates_each_shard_as_its_slice_of_the_whole(cuda):
+    """StateOptimizer._compute subclasses store states through sr_states.cast with the shard start."""
+
+    class SignMomentum(sr_states.StateOptimizer):
+        _state_names = ("momentum_buffer",)
+        _uses_step = False
+
+        def __init__(self, params):
+            super().__init__(params, {"lr": 0.01}, state_dtype=torch.bfloat16, seed=21)
+
+        def _compute(self, p32, g32, states32, group, step):
+            buffer = states32[0] * 0.9 + g32
+            return p32 - group["lr"] * torch.sign(buffer), (buffer,)
+
+    params, grads = _problem(cuda, seed=3)
+    full_params, full_opt = _run(SignMomentum, params, grads, lambda t: t.clone())
+    mesh_shape, placements = (3,), (Shard(0),)
+    for rank in range(3):
+        mesh = _mesh(mesh_shape, rank)
+        shard_params, shard_opt = _run(SignMomentum, params, grads, lambda t: _shard(t, mesh, placements))
+        torch.cuda.synchronize()
+        _compare(full_params, full_opt, shard_params, shard_opt, ("momentum_buffer",), f"rank {rank}")
