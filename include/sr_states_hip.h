@@ -95,7 +95,9 @@ typedef struct sr_adamw_hparams {
   float one_minus_beta1;  /* f32(1 - beta1) */
   float one_minus_beta2;  /* f32(1 - beta2) */
   float neg_step_size;    /* f32(-lr / (1 - beta1^step)) */
-  float correction2_sqrt; /* f32(sqrt(1 - beta2^step)) */
+  float correction2_sqrt; /* f32(sqrt(1 - beta2^step)), in [2^-27, 1] for
+                             0 <= beta2 < 1 and step >= 1; the AdamW entry
+                             points fail with SR_ERR_ARGUMENT outside it */
   float decay;            /* f32(1 - lr * weight_decay) */
   float eps;              /* f32(eps) */
 } sr_adamw_hparams;
@@ -159,7 +161,9 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n,
  * total_tiles row indices (tile_rows[t] = the row whose range holds t).
  * `row_scalars` is NULL when every row has the same AdamW step (hp then
  * holds its scalars), or a device array of 2 * nrows floats holding each
- * row's (neg_step_size, correction2_sqrt); the other scalars come from hp.
+ * row's (neg_step_size, correction2_sqrt), each correction2_sqrt in
+ * [2^-27, 1] as in hp (not checked: the table is device memory); the other
+ * scalars come from hp.
  * The reference launches once per distinct step instead
  * (sr_states/triton/_multi_tensor.py:22-36); the per-row pair keeps one
  * launch per bucket with the same FP32 scalars per row.

@@ -106,7 +106,12 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 
 sr::AdamWScalars adamw_scalars(const sr_adamw_hparams& h) {
   return {h.beta1, h.beta2, h.one_minus_beta1, h.one_minus_beta2,
-          h.neg_step_size, h.correction2_sqrt, h.decay, h.eps};
+          h.neg_step_size, h.correction2_sqrt, h.decay, h.eps, 1.0f / h.correction2_sqrt};
+}
+
+// correction2_sqrt in [2^-27, 1] (sr_math.h, div_by_constant); NaN fails.
+bool valid_correction(const sr_adamw_hparams& h) {
+  return h.correction2_sqrt >= sr::kMinCorrection2Sqrt && h.correction2_sqrt <= 1.0f;
 }
 
 }  // namespace
@@ -159,6 +164,8 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n, int p_dty
   if (me < 0 || ve < 0) return fail(SR_ERR_ARGUMENT, "unsupported state dtype or rule");
   if (!valid_block(block_size)) return fail(SR_ERR_ARGUMENT, "invalid block size %d", block_size);
   if (!hp) return fail(SR_ERR_ARGUMENT, "null hyperparameters");
+  if (!valid_correction(*hp))
+    return fail(SR_ERR_ARGUMENT, "correction2_sqrt %g outside [2^-27, 1]", (double)hp->correction2_sqrt);
   if (n < 0) return fail(SR_ERR_ARGUMENT, "negative element count");
   if (n == 0) return SR_OK;
   if (!p || !g || !m || !v) return fail(SR_ERR_ARGUMENT, "null pointer");
@@ -194,6 +201,8 @@ int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, const float* r
   if (me < 0 || ve < 0) return fail(SR_ERR_ARGUMENT, "unsupported state dtype or rule");
   if (!valid_block(block_size)) return fail(SR_ERR_ARGUMENT, "invalid block size %d", block_size);
   if (!hp || !rows || !tile_rows) return fail(SR_ERR_ARGUMENT, "null argument");
+  if (!valid_correction(*hp))
+    return fail(SR_ERR_ARGUMENT, "correction2_sqrt %g outside [2^-27, 1]", (double)hp->correction2_sqrt);
   if (nrows < 1) return fail(SR_ERR_ARGUMENT, "row count %d below 1", nrows);
   if (total_tiles == 0) return fail(SR_ERR_ARGUMENT, "empty tile range");
   sr::AdamWArgs a{};

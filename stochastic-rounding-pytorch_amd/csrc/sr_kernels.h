@@ -226,14 +226,26 @@ __device__ __forceinline__ void adamw_vector(char* p, const char* g, char* m, ch
   load_vec<ME>(m, i, rm);
   load_vec<VE>(v, i, rv);
   const uint32_t base = static_cast<uint32_t>(i);
+  float mo[E], vo[E], root[E];
+  bool tiny = false;
 #pragma unroll
   for (int k = 0; k < E; ++k) {
-    float po, mo, vo;
-    adamw_update(decode<PE>(rp[k]), decode<GE>(rg[k]), decode<ME>(rm[k]), decode<VE>(rv[k]), s,
-                 po, mo, vo);
-    rp[k] = encode<PE>(po, 0);
-    rm[k] = encode<ME>(mo, cm + base + k);
-    rv[k] = encode<VE>(vo, cv + base + k);
+    adamw_moments(decode<GE>(rg[k]), decode<ME>(rm[k]), decode<VE>(rv[k]), s, mo[k], vo[k]);
+    root[k] = sqrt_rn_wide(vo[k]);
+    tiny |= sqrt_needs_library(vo[k]);
+  }
+  // One branch for the lane's E square roots; whole waves skip it.
+  if (tiny) {
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      if (sqrt_needs_library(vo[k])) root[k] = sqrt_library(vo[k]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    rp[k] = encode<PE>(adamw_parameter(decode<PE>(rp[k]), mo[k], root[k], s), 0);
+    rm[k] = encode<ME>(mo[k], cm + base + k);
+    rv[k] = encode<VE>(vo[k], cv + base + k);
   }
   store_vec<PE>(p, i, rp);
   store_vec<ME>(m, i, rm);
@@ -263,6 +275,7 @@ __global__ __launch_bounds__(kMaxBlock) void adamw_kernel(const AdamWArgs a) {
   if (a.row_scalars) {
     s.neg_step_size = a.row_scalars[2 * row];
     s.correction2_sqrt = a.row_scalars[2 * row + 1];
+    s.inv_correction2_sqrt = 1.0f / s.correction2_sqrt;
   }
   char* p = reinterpret_cast<char*>(r.ptr[0]);
   const char* g = reinterpret_cast<const char*>(r.ptr[1]);

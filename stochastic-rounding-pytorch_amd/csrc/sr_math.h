@@ -389,7 +389,77 @@ SR_HD float decode(uint32_t v) {
 struct AdamWScalars {
   float beta1, beta2, one_minus_beta1, one_minus_beta2;
   float neg_step_size, correction2_sqrt, decay, eps;
+  float inv_correction2_sqrt;  // RN(1 / correction2_sqrt)
 };
+
+// Domain of correction2_sqrt = f32(sqrt(1 - beta2^t)) for 0 <= beta2 < 1
+// (a double) and t >= 1: 1 - beta2^t >= 2^-53, so it lies in [2^-27, 1].
+constexpr float kMinCorrection2Sqrt = 0x1p-27f;
+
+// IEEE square root, correctly rounded, for |v| >= 2^-96, zero, infinite
+// and NaN v.  On the device: the hardware estimate, which is within one
+// ulp, corrected to the nearest by the signs of v - s*(s - ulp) and
+// v - s*(s + ulp) (s*(s -/+ ulp) is the square of the midpoint below/above
+// s, less ulp^2/4, and no float lies strictly between the two).  Below
+// 2^-96 the residuals can lose their sign: sqrt_needs_library() marks those
+// inputs, for which the caller takes sqrtf.  Checked, with that fallback,
+// against sqrtf on every FP32 input.
+SR_HD float sqrt_rn_wide(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float s = __builtin_amdgcn_sqrtf(v);
+  const float below = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, s) - 1u);
+  const float above = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, s) + 1u);
+  const float down = fmaf(-below, s, v) <= 0.0f ? below : s;
+  return fmaf(-above, s, v) > 0.0f ? above : down;
+#else
+  return sqrtf(v);
+#endif
+}
+
+SR_HD bool sqrt_needs_library(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_fabsf(v) < 0x1p-96f && v != 0.0f;
+#else
+  (void)v;
+  return false;
+#endif
+}
+
+// sqrtf behind a side effect the compiler may not hoist, so that the
+// library's scaled sequence stays behind its branch instead of being
+// computed for every input and selected.
+SR_HD float sqrt_library(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __asm__ volatile("" : "+v"(v));
+#endif
+  return sqrtf(v);
+}
+
+// Correctly rounded square root of any float.
+SR_HD float sqrt_rn(float v) {
+  float root = sqrt_rn_wide(v);
+  if (sqrt_needs_library(v)) root = sqrt_library(v);
+  return root;
+}
+
+// x / c, correctly rounded, for c in [2^-27, 1] with r = RN(1/c), and x
+// zero, infinite, NaN or in [2^-75, 2^64] (every square root of a float).
+// On the device: q0 = RN(x r) and one correction by the exact remainder
+// x - q0 c (Markstein's step).  Scaling x or c by a power of two scales
+// every intermediate exactly in that domain, so agreement on every pair of
+// significands is agreement everywhere; a device check covers all 2^46
+// pairs.  Zero, infinite and NaN quotients keep q0, as x / c gives them.
+SR_HD float div_by_constant(float x, float c, float r) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float q0 = x * r;
+  const float q = fmaf(fmaf(-q0, c, x), r, q0);
+  constexpr int kFinite = 8 | 16 | 128 | 256;  // negative/positive normal and subnormal
+  return __builtin_amdgcn_classf(q0, kFinite) ? q : q0;
+#else
+  (void)r;
+  return x / c;
+#endif
+}
 
 // sr_states/reference/adamw.py:86-96:
 //   m' = m*beta1 + (1-beta1)*g          -> fma(g, 1-beta1, m*beta1)
@@ -397,19 +467,29 @@ struct AdamWScalars {
 //   den = sqrt(v') / sqrt(1-beta2^t) + eps
 //   p' = p*(1-lr*wd) + (-lr/(1-beta1^t) * m') / den
 // Every operation is rounded to FP32 on its own; division and square root
-// are IEEE correctly rounded.  The parameter uses the unrounded m'.
-SR_HD void adamw_update(float p, float g, float m, float v, const AdamWScalars& s,
-                        float& p_out, float& m_out, float& v_out) {
+// are IEEE correctly rounded (the division by sqrt(1-beta2^t) through its
+// reciprocal, exactly).  The parameter uses the unrounded m'.
+SR_HD void adamw_moments(float g, float m, float v, const AdamWScalars& s, float& m_out,
+                         float& v_out) {
   const float m_scaled = m * s.beta1;
   m_out = fmaf(g, s.one_minus_beta1, m_scaled);
   const float g_scaled = s.one_minus_beta2 * g;
   const float v_scaled = v * s.beta2;
   v_out = fmaf(g_scaled, g, v_scaled);
-  const float root = sqrtf(v_out);
-  const float den = root / s.correction2_sqrt + s.eps;
+}
+
+// The parameter from the unrounded m' and root = sqrt(v').
+SR_HD float adamw_parameter(float p, float m_out, float root, const AdamWScalars& s) {
+  const float den = div_by_constant(root, s.correction2_sqrt, s.inv_correction2_sqrt) + s.eps;
   const float numer = s.neg_step_size * m_out;
   const float p_decayed = p * s.decay;
-  p_out = p_decayed + numer / den;
+  return p_decayed + numer / den;
+}
+
+SR_HD void adamw_update(float p, float g, float m, float v, const AdamWScalars& s,
+                        float& p_out, float& m_out, float& v_out) {
+  adamw_moments(g, m, v, s, m_out, v_out);
+  p_out = adamw_parameter(p, m_out, sqrt_rn(v_out), s);
 }
 
 struct SgdmScalars {

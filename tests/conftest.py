@@ -26,7 +26,8 @@ def pytest_configure(config):
     built = (PACKAGE_DIR / "sr_states").glob("_group_walk*.so")
     library = PACKAGE_DIR / "sr_states" / "libsr_states_hip.so"
     checks = [ROOT / "tests" / "native" / name
-              for name in ("libbf16_sr_check.so", "libstream_ceiling.so", "libminifloat_check.so")]
+              for name in ("libbf16_sr_check.so", "libstream_ceiling.so", "libminifloat_check.so",
+                         "libdivsqrt_check.so")]
     if not all(check.exists() for check in checks) and not torch.cuda.is_available():
         import importlib.util
 

@@ -6,6 +6,8 @@
   check of bf16_sr_check.hip;
 - tests/native/libminifloat_check.so, the exhaustive check of the device
   minifloat encoders of minifloat_check.hip;
+- tests/native/libdivsqrt_check.so, the exhaustive check of the AdamW
+  update's square root and constant-divisor division of divsqrt_check.hip;
 - tests/native/libstream_ceiling.so, the trivial-math kernel of
   stream_ceiling.hip that measures the bandwidth ceiling of the fused
   update's access pattern (bench.py and tests/test_gpu_stream_ceiling.py).
@@ -26,8 +28,9 @@ ROOT = HERE.parents[1]
 CHECK_LIBRARY = HERE / "libbf16_sr_check.so"
 CEILING_LIBRARY = HERE / "libstream_ceiling.so"
 MINIFLOAT_LIBRARY = HERE / "libminifloat_check.so"
+DIVSQRT_LIBRARY = HERE / "libdivsqrt_check.so"
 LIBRARIES = {CHECK_LIBRARY: HERE / "bf16_sr_check.hip", CEILING_LIBRARY: HERE / "stream_ceiling.hip",
-             MINIFLOAT_LIBRARY: HERE / "minifloat_check.hip"}
+             MINIFLOAT_LIBRARY: HERE / "minifloat_check.hip", DIVSQRT_LIBRARY: HERE / "divsqrt_check.hip"}
 
 
 def _package_build():

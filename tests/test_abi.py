@@ -76,6 +76,17 @@ def test_invalid_arguments_fail_before_any_device_work():
     assert b"FP32 or BF16" in lib.sr_last_error()
     assert lib.sr_adamw_multi(None, None, None, 1, 1, 0, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, 256, None) == 1
     assert b"null argument" in lib.sr_last_error()
+    # The division by sqrt(1 - beta2^t) is exact for values in [2^-27, 1],
+    # which every 0 <= beta2 < 1 and step >= 1 give; zero (hp's default),
+    # NaN and values above 1 are refused.
+    for correction in (0.0, 2.0**-28, 1.0000001, float("nan")):
+        hp.correction2_sqrt = correction
+        for call in (
+            lambda: lib.sr_adamw_step(None, None, None, None, 8, 0, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, 256, None),
+            lambda: lib.sr_adamw_multi(1, 1, None, 1, 1, 0, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, 256, None),
+        ):
+            assert call() == 1
+            assert b"correction2_sqrt" in lib.sr_last_error()
     sp = _lib.SgdmHparams()
     assert lib.sr_sgdm_multi(None, None, 0, 1, 0, 0, 7, 1, ctypes.byref(sp), 0, 0, 256, None) == 1
     assert b"unsupported state" in lib.sr_last_error()
