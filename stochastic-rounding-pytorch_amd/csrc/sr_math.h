@@ -266,27 +266,40 @@ SR_HD uint32_t minifloat_bits_fast(uint32_t b, uint32_t hash) {
     const uint32_t enc = nearest_convert<F>(a | sign);
     return nan ? (F::kNan | (sign >> (32 - F::kWidth))) : enc;
   }
+  // D dropped significand bits: 23 - M on normal results, one more per
+  // binade below the smallest normal.  The code works with s = 32 - D and
+  // the complemented hash: (~hash) >> k = (2^(32-k) - 1) - (hash >> k).
   // An FP32 subnormal (E = 0) is far below F's smallest subnormal; taking
   // its exponent as 0 instead of 1 keeps it in the second branch, where it
-  // never rounds up, as in the integer form.  The two branches (and the
-  // t < 24 test) stay real branches: waves whose elements all take one
-  // side skip the other, which measured 3-6% faster on FP8 casts than
-  // computing both sides with selects.
+  // never rounds up, as in the integer form.  The two branches stay real
+  // branches: waves whose elements all take one side skip the other, which
+  // measured 3-6% faster on FP8 casts than computing both sides with
+  // selects.
   const int E = static_cast<int>(a >> 23);
-  const int below = F::kEmin + 127 - E;  // binades below the smallest normal
-  const int D = 23 - F::kM + (below > 0 ? below : 0);
-  uint32_t r;
-  if (D <= 23) {
-    const uint32_t mask = (1u << D) - 1u;
-    r = (a + mask - ((hash >> 8) >> (24 - D))) & ~mask;
-  } else {
-    const uint32_t sig = (a & 0x007FFFFFu) | 0x00800000u;
-    const int t = D - 24;
-    const bool up = t < 24 && (hash >> 8) < (sig >> t);
-    r = up ? static_cast<uint32_t>(F::kEmin - F::kM + 127) << 23 : 0u;  // 2^(EMIN-M) or 0
+  const int s_below = E - (118 + F::kEmin - F::kM);
+  const int s = s_below < 9 + F::kM ? s_below : 9 + F::kM;
+  const uint32_t sign_bit = sign >> (32 - F::kWidth);
+  if (s >= 9) {  // D <= 23
+    // With T = (hash >> 8) >> (24 - D) = hash >> s and mask = 2^D - 1:
+    // mask - T = ~hash >> s, and mask = 0xFFFFFFFF >> s.
+    const uint32_t r = (a + (~hash >> s)) & ~(0xFFFFFFFFu >> s);
+    const uint32_t enc = nearest_convert<F>(r | sign);  // exact: r is on the grid
+    return nan ? (F::kNan | sign_bit) : enc;            // NaN has E = 255: only here
   }
-  const uint32_t enc = nearest_convert<F>(r | sign);  // exact: r is on the grid
-  return nan ? (F::kNan | (sign >> (32 - F::kWidth))) : enc;
+  // D >= 24: 0, or the smallest subnormal (encoding 1) when the random
+  // value's upper 24 bits fall below sig / 2^(D - 24); no NaN reaches here.
+  // Shifts of 24 to 31 leave nothing of the 24-bit significand, so D - 24
+  // is clamped to 31 instead of tested.
+#if defined(__HIP_DEVICE_COMPILE__)
+  // The compiler drops the skip over a divergent block this short, so
+  // waves with no such element would still issue it; an asm statement
+  // (even an empty one) keeps the skip.
+  __asm__ volatile("");
+#endif
+  const uint32_t sig = (a & 0x007FFFFFu) | 0x00800000u;
+  const int t = 8 - s;  // D - 24
+  const bool up = (hash >> 8) < (sig >> (t < 31 ? t : 31));
+  return sign_bit | (up ? 1u : 0u);
 }
 
 // The minifloat encoders: the integer form on the host, its bit-exact
