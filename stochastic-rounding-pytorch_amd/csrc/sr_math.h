@@ -3,9 +3,10 @@
 // Everything here is a pure function of its arguments, usable on the host
 // (key derivation, CPU-side unit checks) and on gfx950.  Encoders work on the
 // IEEE-754 bit patterns with integer ALU, except that the device finishes
-// BF16 stochastic rounding with gfx950's stochastic convert and the minifloat
-// encodings with a hardware convert of an exactly representable value; both
-// are checked exhaustively against the integer forms on the device.  The FP32 recurrences use explicit fmaf() exactly where the
+// BF16 stochastic rounding with gfx950's stochastic convert, BF16 nearest
+// rounding with its nearest convert, and the minifloat encodings with a
+// hardware convert of an exactly representable value; all are checked
+// exhaustively against the integer forms on the device.  The FP32 recurrences use explicit fmaf() exactly where the
 // reference's eager CPU kernels fuse, and must be compiled with
 // -ffp-contract=off so that no other multiply-add is contracted.
 #pragma once
@@ -147,6 +148,19 @@ SR_HD uint32_t bf16_sr(uint32_t b, uint32_t hash) {
 SR_HD uint32_t bf16_rn_bits(uint32_t b) {
   if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
   return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+// bf16_rn_bits on the device: gfx950's v_cvt_pk_bf16_f32 rounds to nearest
+// even in the kernels' rounding mode and keeps subnormals; NaN becomes the
+// reference's 0x7FC0.  Checked against bf16_rn_bits on every FP32 input.
+SR_HD uint32_t bf16_rn(uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float x = __builtin_bit_cast(float, b);
+  const uint32_t rounded = __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+  return x != x ? 0x7FC0u : rounded;
+#else
+  return bf16_rn_bits(b);
+#endif
 }
 
 // Minifloat formats: mantissa bits M, minimum normal exponent EMIN, FP32
@@ -321,7 +335,7 @@ SR_HD uint32_t encode(float x, uint32_t counter) {
   if constexpr (ENC == ENC_F32) {
     return b;
   } else if constexpr (ENC == ENC_BF16_RN) {
-    return bf16_rn_bits(b);
+    return bf16_rn(b);
   } else if constexpr (ENC == ENC_BF16_SR) {
     return bf16_sr(b, h32(counter));
   } else if constexpr (ENC == ENC_F16_RN) {

@@ -7,6 +7,8 @@
 //   sweep 2: for twelve upper halves (zeros, subnormals, ordinary values, the
 //            largest finite value, Inf and NaN patterns, both signs), every
 //            pair of low input half and 16-bit random value.
+// The nearest encoder's device path sr::bf16_rn (v_cvt_pk_bf16_f32) is
+// compared with sr::bf16_rn_bits on every FP32 input (sr_check_bf16_rn).
 // Built by __graft_entry__.build() into tests/native/libbf16_sr_check.so and
 // run by tests/test_gpu_bf16_sr_check.py.
 #include <hip/hip_runtime.h>
@@ -42,6 +44,12 @@ __global__ void every_input(uint32_t base, unsigned long long* counters) {
   add(counters, mismatches, 5);
 }
 
+// One launch covers 2^31 inputs starting at `base`.
+__global__ void every_input_nearest(uint32_t base, unsigned long long* counters) {
+  const uint32_t b = base + blockIdx.x * blockDim.x + threadIdx.x;
+  add(counters, sr::bf16_rn(b) != sr::bf16_rn_bits(b), 1);
+}
+
 // One launch covers 2^15 random values x 2^16 low halves for upper half `hi`;
 // each thread also takes the random value with bit 15 set.
 __global__ void every_pair(uint32_t hi, unsigned long long* counters) {
@@ -72,6 +80,24 @@ extern "C" int sr_check_bf16_sr(unsigned long long* counters_host) {
   for (uint32_t hi : highs) {
     if (err != hipSuccess) break;
     hipLaunchKernelGGL(every_pair, grid, block, 0, 0, hi, counters);
+    err = hipGetLastError();
+  }
+  if (err == hipSuccess) err = hipDeviceSynchronize();
+  if (err == hipSuccess) {
+    err = hipMemcpy(counters_host, counters, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  }
+  if (counters) (void)hipFree(counters);
+  return static_cast<int>(err);
+}
+
+// Every FP32 input through the nearest encoder: counters_host[0] =
+// mismatches, [1] = comparisons (2^32).  Returns 0 or a hipError_t.
+extern "C" int sr_check_bf16_rn(unsigned long long* counters_host) {
+  unsigned long long* counters = nullptr;
+  hipError_t err = hipMalloc(&counters, 2 * sizeof(unsigned long long));
+  if (err == hipSuccess) err = hipMemset(counters, 0, 2 * sizeof(unsigned long long));
+  for (uint32_t half = 0; err == hipSuccess && half < 2; ++half) {
+    hipLaunchKernelGGL(every_input_nearest, dim3(1u << 23), dim3(256), 0, 0, half << 31, counters);
     err = hipGetLastError();
   }
   if (err == hipSuccess) err = hipDeviceSynchronize();

@@ -32,3 +32,17 @@ def test_hardware_sr_convert_matches_the_reference_rule_exhaustively(cuda):
     mismatches, comparisons = counters[0], counters[1]
     assert comparisons == 5 * 2**32 + 12 * 2**32
     assert mismatches == 0
+
+
+def test_hardware_nearest_convert_matches_the_reference_rule_on_every_input(cuda):
+    """sr::bf16_rn (v_cvt_pk_bf16_f32, NaN as 0x7FC0) against the integer nearest-even form."""
+    import torch  # noqa: F401  (load the HIP runtime first)
+
+    assert LIBRARY.exists(), f"{LIBRARY} is not built (tests/native/build_checks.py)"
+    check = ctypes.CDLL(str(LIBRARY))
+    check.sr_check_bf16_rn.restype = ctypes.c_int
+    check.sr_check_bf16_rn.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
+    counters = (ctypes.c_ulonglong * 2)()
+    assert check.sr_check_bf16_rn(counters) == 0
+    assert counters[1] == 2**32
+    assert counters[0] == 0, f"{counters[0]} of 2^32 inputs differ"
