@@ -16,11 +16,12 @@
 //   ``layout`` (bytes) fixes every tensor's Python type, element count, dtype,
 //   device, contiguity and sizes, every parameter's and state's address, and
 //   which parameters have gradients; gradient addresses are left out.  A
+//   DTensor is described by its spec's identity and its local shard.  A
 //   validated step vouches only for the types it saw.  None means "take the
 //   validating path": an object that is not a tensor, a missing state, a
-//   non-strided tensor, one with elements but no memory (wrapper
-//   subclasses), a stored step that is not a non-negative int, or no
-//   parameter with a gradient.  When uses_step is true and every parameter
+//   non-strided tensor, one with elements but no memory (wrapper subclasses
+//   other than DTensor), a stored step that is not a non-negative int, or
+//   no parameter with a gradient.  When uses_step is true and every parameter
 //   with a gradient stores the same step (0 when absent), ``step`` is that
 //   value and ``steps`` is None; when they differ, ``step`` is None and
 //   ``steps`` lists them in group order.  Both are None when uses_step is
@@ -49,8 +50,10 @@
 
 namespace {
 
-PyObject* g_grad = nullptr;  // interned "grad"
-PyObject* g_step = nullptr;  // interned "step"
+PyObject* g_grad = nullptr;   // interned "grad"
+PyObject* g_step = nullptr;   // interned "step"
+PyObject* g_local = nullptr;  // interned "_local_tensor"
+PyObject* g_spec = nullptr;   // interned "_spec"
 
 // Everything one walk collects.
 struct Walk {
@@ -60,14 +63,59 @@ struct Walk {
   std::vector<int64_t> steps;      // stored step per parameter with a gradient
 };
 
+// Owned reference released at scope exit.
+struct Ref {
+  PyObject* obj;
+  explicit Ref(PyObject* o) : obj(o) {}
+  Ref(const Ref&) = delete;
+  Ref& operator=(const Ref&) = delete;
+  ~Ref() { Py_XDECREF(obj); }
+};
+
+bool describe(PyObject* obj, Walk& w, bool gradient, PyObject* parameter_spec = nullptr);
+
+// A DTensor: a tensor subclass whose data is the `_local_tensor` it carries,
+// laid out by its `_spec` (mesh, placements, global shape).
+bool is_distributed(PyObject* obj) {
+  return !THPVariable_CheckExact(obj) && PyObject_HasAttr(obj, g_local);
+}
+
+// A DTensor parameter's or state's words: its Python type, the identity of
+// its spec, and its local shard's words.  The spec object is replaced
+// whenever the mesh, placements or global shape change, and the optimizer
+// keeps parameters and states (and so their specs) alive between steps, so
+// an unchanged identity vouches for the shard start and the placement
+// checks of the validated step.  A DTensor gradient is new every step: its
+// spec must be the parameter's or equal to it, checked here, and only its
+// type and local shard enter the words.
+bool describe_distributed(PyObject* obj, Walk& w, bool gradient, PyObject* parameter_spec) {
+  Ref local(PyObject_GetAttr(obj, g_local));
+  if (local.obj == nullptr || !THPVariable_Check(local.obj)) return false;
+  Ref spec(PyObject_GetAttr(obj, g_spec));
+  if (spec.obj == nullptr) return false;
+  w.words.push_back(static_cast<int64_t>(reinterpret_cast<intptr_t>(Py_TYPE(obj))));
+  if (gradient) {
+    if (parameter_spec == nullptr) return false;
+    if (spec.obj != parameter_spec && PyObject_RichCompareBool(spec.obj, parameter_spec, Py_EQ) != 1) {
+      return false;
+    }
+  } else {
+    w.words.push_back(static_cast<int64_t>(reinterpret_cast<intptr_t>(spec.obj)));
+  }
+  return describe(local.obj, w, gradient);
+}
+
 // Appends the words that fix one tensor's view: Python type, address (unless
 // it is a gradient, whose address goes to w.gradients), element count, dtype,
-// device, contiguity, rank and sizes; and the tensor's byte span.  False when
-// the object is not a tensor or has no strided memory to describe.
-bool describe(PyObject* obj, Walk& w, bool gradient) {
+// device, contiguity, rank and sizes; and the tensor's byte span.  A DTensor
+// is described through its local shard.  False when the object is not a
+// tensor or has no strided memory to describe.
+bool describe(PyObject* obj, Walk& w, bool gradient, PyObject* parameter_spec) {
   if (!THPVariable_Check(obj)) return false;
   try {
     const at::Tensor& t = THPVariable_Unpack(obj);
+    // Plain tensors and parameters skip the attribute lookup.
+    if (is_distributed(obj)) return describe_distributed(obj, w, gradient, parameter_spec);
     if (!t.defined() || t.layout() != at::kStrided || !t.has_storage()) return false;
     const auto sizes = t.sizes();
     const at::Device device = t.device();
@@ -108,15 +156,6 @@ PyObject* parameter_state(PyObject* state, PyObject* parameter) {
   return entry;
 }
 
-// Owned reference released at scope exit.
-struct Ref {
-  PyObject* obj;
-  explicit Ref(PyObject* o) : obj(o) {}
-  Ref(const Ref&) = delete;
-  Ref& operator=(const Ref&) = delete;
-  ~Ref() { Py_XDECREF(obj); }
-};
-
 // One parameter with a gradient: its words, spans and stored step.
 bool walk_parameter(PyObject* parameter, PyObject* gradient, PyObject* state, PyObject* names,
                     bool uses_step, Walk& w, int64_t& step, PyObject* entries) {
@@ -126,7 +165,8 @@ bool walk_parameter(PyObject* parameter, PyObject* gradient, PyObject* state, Py
   Py_INCREF(entry);
   if (PyList_Append(entries, entry) != 0) return false;
   w.words.push_back(2 + PyTuple_GET_SIZE(names));
-  if (!describe(parameter, w, false) || !describe(gradient, w, true)) return false;
+  Ref parameter_spec(is_distributed(parameter) ? PyObject_GetAttr(parameter, g_spec) : nullptr);
+  if (!describe(parameter, w, false) || !describe(gradient, w, true, parameter_spec.obj)) return false;
   for (Py_ssize_t k = 0; k < PyTuple_GET_SIZE(names); ++k) {
     PyObject* tensor = PyDict_GetItemWithError(entry, PyTuple_GET_ITEM(names, k));
     if (tensor == nullptr || !describe(tensor, w, false)) return false;
@@ -277,6 +317,8 @@ PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_group_walk",
 PyMODINIT_FUNC PyInit__group_walk() {
   g_grad = PyUnicode_InternFromString("grad");
   g_step = PyUnicode_InternFromString("step");
-  if (g_grad == nullptr || g_step == nullptr) return nullptr;
+  g_local = PyUnicode_InternFromString("_local_tensor");
+  g_spec = PyUnicode_InternFromString("_spec");
+  if (g_grad == nullptr || g_step == nullptr || g_local == nullptr || g_spec == nullptr) return nullptr;
   return PyModule_Create(&kModule);
 }

@@ -404,3 +404,42 @@ def test_alternating_gradient_addresses_reuse_their_own_records(recorder, monkey
     assert [opt.state[p]["step"] for p in params] == [10, 10, 10]
     tables = {id(launch["tables"]) for launch in recorder[1:]}
     assert len(tables) == 2
+
+
+def _dtensor_group(rank=1, n=3):
+    """A group of DTensor parameters (Shard(0) on a two-rank mesh, as rank ``rank``)."""
+    from test_dtensor import _dtensor, _mesh
+    from torch.distributed.tensor import Shard
+
+    mesh = _mesh((2,), rank)
+    params = [torch.nn.Parameter(_dtensor(torch.randn(7, 3), mesh, (Shard(0),))) for _ in range(n)]
+    for p in params:
+        p.grad = _dtensor(torch.randn(7, 3), mesh, (Shard(0),))
+    state = {p: {"exp_avg": torch.zeros_like(p), "exp_avg_sq": torch.zeros_like(p)} for p in params}
+    return mesh, params, state
+
+
+def test_dtensor_groups_are_described_by_their_local_shards():
+    """Parameters and states by spec identity and local shard; gradients by local shard."""
+    from test_dtensor import _dtensor
+    from torch.distributed.tensor import DTensor, Partial, Shard
+
+    mesh, params, state = _dtensor_group()
+    first = _sig(params, state)
+    assert first is not None
+    local_grads = [p.grad._local_tensor.data_ptr() for p in params]
+    assert list(np.frombuffer(first[4], dtype=np.int64)) == local_grads
+    # A new gradient DTensor with an equal spec (a new spec object): same
+    # layout, new gradient addresses.
+    for p in params:
+        p.grad = _dtensor(torch.randn(7, 3), mesh, (Shard(0),))
+    second = _sig(params, state)
+    assert second[0] == first[0] and second[4] != first[4]
+    # A gradient whose placements differ from its parameter's is the
+    # validating path's to refuse.
+    params[1].grad = DTensor.from_local(torch.ones(7, 3), mesh, (Partial(),), run_check=False)
+    assert _sig(params, state) is None
+    params[1].grad = _dtensor(torch.randn(7, 3), mesh, (Shard(0),))
+    # A state replaced by another DTensor changes the layout.
+    state[params[2]]["exp_avg"] = torch.zeros_like(params[2])
+    assert _sig(params, state)[0] != second[0]
