@@ -89,16 +89,20 @@ template <int OUT>
 __global__ __launch_bounds__(kCastBlock) void cast_streams(const void* x, void* y, uint32_t tiles) {
   const uint32_t t = sr::tile_of(blockIdx.y * gridDim.x + blockIdx.x, tiles);
   if (t >= tiles) return;
-  const uint64_t i = static_cast<uint64_t>(t) * kCastTile + threadIdx.x * kCastLanes;
-  const word4 a = load<4>(x, i), b = load<4>(x, i + kLanes);
+  // The cast's lane layout: two groups of 4 elements a workgroup-width apart.
+  const uint64_t i0 = static_cast<uint64_t>(t) * kCastTile + threadIdx.x * kLanes;
+  const uint64_t i1 = i0 + kCastBlock * kLanes;
+  const word4 a = load<4>(x, i0), b = load<4>(x, i1);
   if constexpr (OUT == 2) {
-    const word4 out = {(a.x >> 16) | (a.y & 0xFFFF0000u), (a.z >> 16) | (a.w & 0xFFFF0000u),
-                       (b.x >> 16) | (b.y & 0xFFFF0000u), (b.z >> 16) | (b.w & 0xFFFF0000u)};
-    __builtin_nontemporal_store(out, reinterpret_cast<word4*>(static_cast<char*>(y) + i * 2));
+    __builtin_nontemporal_store(word2{(a.x >> 16) | (a.y & 0xFFFF0000u), (a.z >> 16) | (a.w & 0xFFFF0000u)},
+                                reinterpret_cast<word2*>(static_cast<char*>(y) + i0 * 2));
+    __builtin_nontemporal_store(word2{(b.x >> 16) | (b.y & 0xFFFF0000u), (b.z >> 16) | (b.w & 0xFFFF0000u)},
+                                reinterpret_cast<word2*>(static_cast<char*>(y) + i1 * 2));
   } else {
-    const word2 out = {(a.x >> 24) | ((a.y >> 16) & 0xFF00u) | ((a.z >> 8) & 0xFF0000u) | (a.w & 0xFF000000u),
-                       (b.x >> 24) | ((b.y >> 16) & 0xFF00u) | ((b.z >> 8) & 0xFF0000u) | (b.w & 0xFF000000u)};
-    __builtin_nontemporal_store(out, reinterpret_cast<word2*>(static_cast<char*>(y) + i));
+    __builtin_nontemporal_store((a.x >> 24) | ((a.y >> 16) & 0xFF00u) | ((a.z >> 8) & 0xFF0000u) | (a.w & 0xFF000000u),
+                                reinterpret_cast<uint32_t*>(static_cast<char*>(y) + i0));
+    __builtin_nontemporal_store((b.x >> 24) | ((b.y >> 16) & 0xFF00u) | ((b.z >> 8) & 0xFF0000u) | (b.w & 0xFF000000u),
+                                reinterpret_cast<uint32_t*>(static_cast<char*>(y) + i1));
   }
 }
 
