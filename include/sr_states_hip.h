@@ -57,9 +57,10 @@ enum sr_error {
 /* Elements one lane moves per tile.  A tile is block_size * (this many)
  * consecutive elements of one tensor and is processed by one workgroup.
  * Optimizer launches currently all use SR_LANE_ELEMENTS (FP32 operands move
- * as one 128-bit access per lane) and casts SR_LANE_ELEMENTS_NARROW.
- * sr_lane_elements() returns the width of an optimizer launch; hosts must
- * use it rather than assume a width. */
+ * as one 128-bit access per lane) and casts SR_LANE_ELEMENTS_NARROW (two
+ * groups of four a workgroup-width apart, so that every access instruction
+ * covers a contiguous span).  sr_lane_elements() returns the width of an
+ * optimizer launch; hosts must use it rather than assume a width. */
 #define SR_LANE_ELEMENTS 4
 #define SR_LANE_ELEMENTS_NARROW 8
 
