@@ -3,6 +3,9 @@
 ``python bench.py [--steps K] [--warmup W] [--workload NAME]`` times K
 optimizer steps (one ``AdamWHip.step()`` = one pass of the fused kernel over
 every parameter) after W untimed warmup steps, and prints ONE JSON line.
+K and W default to the workload's own values (100 and 25 for the north
+star; more for short launches, so that the warmup spans the few hundred
+milliseconds in which the GPU raises its clocks).
 
 Default workload ``north_star``: AdamW with stochastically rounded BF16
 moments over the 1.55 G-element multi-tensor set of BASELINE config 4's
@@ -67,6 +70,8 @@ WORKLOADS = {
     # input/output buffer pairs rotate so that 640 MB of traffic passes through
     # the 256 MB last-level cache between reuses of a buffer.
     "c1_cast_bf16": dict(
+        warmup=20000,
+        steps=5000,
         optimizer="cast",
         shapes=[(1 << 24,)],
         p_dtype=torch.float32,
@@ -77,6 +82,8 @@ WORKLOADS = {
         seed=7,
     ),
     "c2_single_2e26": dict(
+        warmup=1500,
+        steps=500,
         optimizer="adamw",
         shapes=[(1 << 26,)],
         p_dtype=torch.float32,
@@ -90,6 +97,8 @@ WORKLOADS = {
     # parameters with BF16 gradients, BF16-SR moments
     # (benchmarks/bench_optimizer_steps.py:33-53).
     "c3_gpt2": dict(
+        warmup=1000,
+        steps=300,
         optimizer="adamw",
         shapes=[(50257, 768), (1024, 768)]
         + [(768,), (768,), (768, 2304), (2304,), (768, 768), (768,), (768,), (768,),
@@ -129,6 +138,56 @@ WORKLOADS = {
         hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
         seed=7,
     ),
+    # The north star's shapes with BF16 parameters and gradients, for three
+    # state formats: the launches where the FP32 update's arithmetic, not
+    # memory, sets the rate.
+    "bf16_params_bf16sr": dict(
+        optimizer="adamw",
+        shapes=C4_BLOCK * 7 + [(32000, 4096)],
+        p_dtype=torch.bfloat16,
+        g_dtype=torch.bfloat16,
+        formats=((torch.bfloat16, "stochastic"), (torch.bfloat16, "stochastic")),
+        grad_std=1e-3,
+        hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
+        seed=7,
+    ),
+    "bf16_params_e4m3_bf16sr": dict(
+        optimizer="adamw",
+        shapes=C4_BLOCK * 7 + [(32000, 4096)],
+        p_dtype=torch.bfloat16,
+        g_dtype=torch.bfloat16,
+        formats=((torch.float8_e4m3fn, "stochastic"), (torch.bfloat16, "stochastic")),
+        grad_std=1e-3,
+        hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
+        seed=7,
+    ),
+    "bf16_params_fp16sr": dict(
+        optimizer="adamw",
+        shapes=C4_BLOCK * 7 + [(32000, 4096)],
+        p_dtype=torch.bfloat16,
+        g_dtype=torch.bfloat16,
+        formats=((torch.float16, "stochastic"), (torch.float16, "stochastic")),
+        grad_std=1e-3,
+        hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
+        seed=7,
+    ),
+    # Stochastic casts of 2^26 values, eight rotating buffer pairs, per output format.
+    **{
+        f"cast_2e26_{name}": dict(
+            warmup=5000,
+            steps=2000,
+            optimizer="cast",
+            shapes=[(1 << 26,)],
+            p_dtype=torch.float32,
+            g_dtype=torch.float32,
+            formats=((dtype, "stochastic"),),
+            grad_std=1.0,
+            hparams={},
+            seed=7,
+        )
+        for name, dtype in (("bf16", torch.bfloat16), ("fp16", torch.float16),
+                            ("e4m3", torch.float8_e4m3fn), ("e5m2", torch.float8_e5m2))
+    },
     # A plain device copy of known size (4 GiB read + 4 GiB written per step);
     # its rocprofv3 FETCH_SIZE / WRITE_SIZE readings calibrate the counters.
     "copy_calibration": dict(
@@ -367,8 +426,10 @@ def load_traffic(workload: str):
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=100)
-    parser.add_argument("--warmup", type=int, default=25)
+    parser.add_argument("--steps", type=int, default=None,
+                        help="timed steps (default: the workload's, 100 for the north star)")
+    parser.add_argument("--warmup", type=int, default=None,
+                        help="untimed warmup steps (default: the workload's, 25 for the north star)")
     parser.add_argument("--workload", choices=sorted(WORKLOADS), default="north_star")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-ceiling", action="store_true",
@@ -383,6 +444,13 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     spec = WORKLOADS[args.workload]
+    # Short launches need many warmup steps: the GPU raises its clocks over
+    # the first few hundred milliseconds of load, and the FP8 casts at 2^26
+    # measured 4.9 TB/s after 25 warmup steps (1.7 ms) against 6.4 after 3000.
+    if args.warmup is None:
+        args.warmup = spec.get("warmup", 25)
+    if args.steps is None:
+        args.steps = spec.get("steps", 100)
     device = torch.device("cuda", 0)
     params, step = build(spec, device)
     elements = sum(p.numel() for p in params)
@@ -427,7 +495,9 @@ def main():
             "adamw": "AdamW-SR step: params updated/sec and achieved HBM GB/s (% of peak), 1 MI355X",
             "sgdm": "SGDM-SR step: params updated/sec and achieved HBM GB/s (% of peak), 1 MI355X",
             "copy": "device copy (counter calibration): elements/sec, 1 MI355X",
-            "cast": "SR cast FP32->BF16: elements/sec and achieved HBM GB/s, 1 MI355X",
+            "cast": "SR cast FP32->{}: elements/sec and achieved HBM GB/s, 1 MI355X".format(
+                {torch.bfloat16: "BF16", torch.float16: "FP16", torch.float8_e4m3fn: "E4M3",
+                 torch.float8_e5m2: "E5M2"}.get(spec["formats"][0][0] if spec["formats"] else None, "")),
         }[spec["optimizer"]],
         "value": elements / (ms_per_step / 1e3),
         "unit": "params/s",
