@@ -65,10 +65,10 @@ def _shard(full, mesh, placements):
                               shape=full.shape, stride=full.stride())
 
 
-def _problem(cuda, seed):
+def _problem(cuda, seed, dtype=torch.float32):
     gen = torch.Generator(device=cuda).manual_seed(seed)
-    params = [torch.randn(shape, device=cuda, generator=gen) * 0.02 for shape in SHAPES]
-    grads = [[torch.randn(shape, device=cuda, generator=gen) * 1e-3 for shape in SHAPES]
+    params = [(torch.randn(shape, device=cuda, generator=gen) * 0.02).to(dtype) for shape in SHAPES]
+    grads = [[(torch.randn(shape, device=cuda, generator=gen) * 1e-3).to(dtype) for shape in SHAPES]
              for _ in range(STEPS)]
     return params, grads
 
@@ -128,9 +128,10 @@ OPTIMIZERS = {
 
 @pytest.mark.parametrize("mesh_shape, placements", MESHES)
 @pytest.mark.parametrize("kind", list(OPTIMIZERS))
-def test_fused_optimizers_update_each_shard_as_its_slice_of_the_whole(cuda, kind, mesh_shape, placements):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_optimizers_update_each_shard_as_its_slice_of_the_whole(cuda, kind, mesh_shape, placements, dtype):
     make, names = OPTIMIZERS[kind]
-    params, grads = _problem(cuda, seed=len(kind) + len(mesh_shape))
+    params, grads = _problem(cuda, seed=len(kind) + len(mesh_shape), dtype=dtype)
     full_params, full_opt = _run(make, params, grads, lambda t: t.clone())
     for rank in range(int(np.prod(mesh_shape))):
         mesh = _mesh(mesh_shape, rank)
