@@ -163,3 +163,29 @@ def test_per_parameter_path_updates_each_shard_as_its_slice_of_the_whole(cuda):
         shard_params, shard_opt = _run(SignMomentum, params, grads, lambda t: _shard(t, mesh, placements))
         torch.cuda.synchronize()
         _compare(full_params, full_opt, shard_params, shard_opt, ("momentum_buffer",), f"rank {rank}")
+
+
+def test_groups_mixing_dtensor_and_plain_parameters(cuda):
+    """One group holding sharded and replicated-as-plain parameters: one launch covers both kinds."""
+    params, grads = _problem(cuda, seed=17)
+    full_params, full_opt = _run(_adamw_bf16_sr, params, grads, lambda t: t.clone())
+    mesh_shape, placements = (3,), (Shard(0),)
+    for rank in range(3):
+        mesh = _mesh(mesh_shape, rank)
+        # Even-indexed parameters sharded, odd ones whole plain tensors.
+        wraps = [(lambda t: _shard(t, mesh, placements)) if k % 2 == 0 else (lambda t: t.clone())
+                 for k in range(len(params))]
+        parameters = [torch.nn.Parameter(wrap(p)) for wrap, p in zip(wraps, params)]
+        opt = _adamw_bf16_sr(parameters)
+        for step_grads in grads:
+            for parameter, wrap, g in zip(parameters, wraps, step_grads):
+                parameter.grad = wrap(g)
+            opt.step()
+        torch.cuda.synchronize()
+        for k, (full, mixed) in enumerate(zip(full_params, parameters)):
+            if k % 2 == 0:
+                _compare([full], full_opt, [mixed], opt, ("exp_avg", "exp_avg_sq"), f"rank {rank}")
+            else:
+                assert_bits_or_nan(mixed.detach(), full.detach(), f"rank {rank}, plain parameter {k}")
+                for name in ("exp_avg", "exp_avg_sq"):
+                    assert_bits_or_nan(opt.state[mixed][name], full_opt.state[full][name], f"{name} {k}")
