@@ -435,7 +435,20 @@ def main():
     parser.add_argument("--no-ceiling", action="store_true",
                         help="skip the access-pattern ceiling measurement")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument("--state-format", default=None, metavar="DTYPE/RULE",
+                        help="store every state of the workload in this format instead, e.g. "
+                             "float8_e4m3fn/stochastic (the reference's nine policies: "
+                             "benchmarks/bench_states.py:21-31)")
     args = parser.parse_args()
+    state_formats = None
+    if args.state_format:
+        if WORKLOADS[args.workload]["optimizer"] not in ("adamw", "sgdm", "cast"):
+            raise SystemExit(f"--state-format does not apply to {args.workload}")
+        dtype_name, _, rule = args.state_format.partition("/")
+        dtype = getattr(torch, dtype_name, None)
+        if not isinstance(dtype, torch.dtype) or rule not in ("nearest", "stochastic"):
+            raise SystemExit(f"--state-format {args.state_format!r}: expected DTYPE/nearest or DTYPE/stochastic")
+        state_formats = ((dtype, rule),) * len(WORKLOADS[args.workload]["formats"])
     if args.gpus != 1:
         raise SystemExit(
             "bench.py measures one GPU: the fused update needs no collective, and each rank "
@@ -444,6 +457,8 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     spec = WORKLOADS[args.workload]
+    if state_formats:
+        spec = {**spec, "formats": state_formats}
     # Short launches need many warmup steps: the GPU raises its clocks over
     # the first few hundred milliseconds of load, and the FP8 casts at 2^26
     # measured 4.9 TB/s after 25 warmup steps (1.7 ms) against 6.4 after 3000.
@@ -488,7 +503,8 @@ def main():
     bpe = bytes_per_element(spec)
     bytes_per_launch = bpe * elements
     achieved = bytes_per_launch / (kernel_ms / 1e3) / 1e9
-    traffic = load_traffic(args.workload)
+    # The committed counters were measured with the workload's own formats.
+    traffic = None if args.state_format else load_traffic(args.workload)
     dtype = "f32"
     result = {
         "metric": {

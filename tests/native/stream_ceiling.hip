@@ -113,6 +113,10 @@ Kernel pick(int g, int m, int v) {
   if (g == 2 && m == 2 && v == 2) return streams<2, 2, 2>;
   if (g == 4 && m == 1 && v == 2) return streams<4, 1, 2>;
   if (g == 4 && m == 2 && v == 0) return streams<4, 2, 0>;
+  if (g == 4 && m == 4 && v == 4) return streams<4, 4, 4>;
+  if (g == 4 && m == 1 && v == 1) return streams<4, 1, 1>;
+  if (g == 4 && m == 4 && v == 0) return streams<4, 4, 0>;
+  if (g == 4 && m == 1 && v == 0) return streams<4, 1, 0>;
   return nullptr;
 }
 
@@ -121,7 +125,8 @@ Kernel pick(int g, int m, int v) {
 // Average milliseconds per launch of the trivial kernel over n elements with
 // a gradient of g_bytes and states of m_bytes and v_bytes per element
 // (v_bytes 0: one state), over `reps` launches after two untimed ones.
-// Supported patterns: (4,2,2), (2,2,2), (4,1,2), (4,2,0).  n must be a
+// Supported patterns: (4,2,2), (2,2,2), (4,1,2), (4,2,0), (4,4,4), (4,1,1),
+// (4,4,0), (4,1,0).  n must be a
 // positive multiple of 512 with n / 512 <= 2^31 - 4096 (the fused
 // launches' tile limit); the grid is laid out as the fused launches lay it
 // out (sr::launch_shape).  Returns 0, or 1 for an

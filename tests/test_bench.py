@@ -51,3 +51,10 @@ def test_more_than_one_gpu_is_refused_with_a_reason():
                             text=True, timeout=300)
     assert result.returncode != 0
     assert "one GPU" in result.stderr or "one GPU" in result.stdout
+
+
+@pytest.mark.parametrize("value", ["float8_e4m3fn/sideways", "float9/stochastic", "bfloat16"])
+def test_state_format_override_is_validated_before_anything_runs(value):
+    result = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--state-format", value],
+                            capture_output=True, text=True, timeout=300)
+    assert result.returncode != 0 and "--state-format" in result.stderr
