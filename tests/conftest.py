@@ -27,7 +27,7 @@ def pytest_configure(config):
     library = PACKAGE_DIR / "sr_states" / "libsr_states_hip.so"
     checks = [ROOT / "tests" / "native" / name
               for name in ("libbf16_sr_check.so", "libstream_ceiling.so", "libminifloat_check.so",
-                         "libdivsqrt_check.so")]
+                         "libdivsqrt_check.so", "abi_c_host")]
     if not all(check.exists() for check in checks) and not torch.cuda.is_available():
         import importlib.util
 
