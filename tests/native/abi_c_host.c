@@ -2,7 +2,8 @@
  *
  * Allocates device buffers with the HIP runtime, runs sr_cast (BF16 and
  * E4M3 stochastic, FP16 nearest), sr_adamw_step (FP32 parameters, BF16-SR
- * moments) and sr_sgdm_step (FP16-SR momentum) on the default stream,
+ * moments), sr_sgdm_step (FP16-SR momentum) and sr_adamw_multi (three rows
+ * with the row table and tile map built here) on the default stream,
  * copies the results back and compares them byte for byte with the C
  * oracle (oracle/sr_oracle.c, test infrastructure linked in as the
  * checker).  Also checks that a bad argument comes back as SR_ERR_ARGUMENT
@@ -134,6 +135,69 @@ int main(void) {
   if (same(host, p, N * 4, "sr_sgdm_step parameter")) return 1;
   if (check_hip(hipMemcpy(host, dm, N * 2, hipMemcpyDeviceToHost), "copy u")) return 1;
   if (same(host, m, N * 2, "sr_sgdm_step momentum")) return 1;
+
+  /* Multi-tensor AdamW: three rows (three parameters of one bucket) carved
+   * out of the device buffers, one with an unaligned start, with the row
+   * table and tile map a C host builds (the layout sr_row documents). */
+  {
+    const int64_t sizes[3] = {4099, 65536, 777};
+    const int64_t starts[3] = {0, 4104, 69641}; /* element offsets; 69641 is not 16-byte aligned */
+    const uint32_t param_index[3] = {0, 3, 4}, shard_start[3] = {0, 1000, 4294967000u};
+    const int lanes = sr_lane_elements(SR_F32, SR_F32, SR_BF16, SR_BF16), block = 128;
+    const uint32_t tile = (uint32_t)(block * lanes);
+    sr_row rows[3];
+    uint32_t tiles = 0;
+    for (int r = 0; r < 3; ++r) {
+      const uint32_t count = (uint32_t)((sizes[r] + tile - 1) / tile);
+      rows[r].ptr[0] = (uint64_t)(uintptr_t)((float*)dp + starts[r]);
+      rows[r].ptr[1] = (uint64_t)(uintptr_t)((float*)dg + starts[r]);
+      rows[r].ptr[2] = (uint64_t)(uintptr_t)((uint16_t*)dm + starts[r]);
+      rows[r].ptr[3] = (uint64_t)(uintptr_t)((uint16_t*)dv + starts[r]);
+      rows[r].numel = sizes[r];
+      rows[r].tile_begin = tiles;
+      rows[r].tile_end = tiles + count;
+      rows[r].param_index = param_index[r];
+      rows[r].shard_start = shard_start[r];
+      rows[r].flags = (starts[r] % 8 == 0) ? SR_ROW_VECTOR : 0u; /* 16-byte aligned FP32 and BF16 */
+      rows[r].reserved = 0;
+      tiles += count;
+    }
+    uint32_t* tile_rows = malloc(tiles * sizeof(uint32_t));
+    if (!tile_rows) return 1;
+    for (int r = 0; r < 3; ++r)
+      for (uint32_t t = rows[r].tile_begin; t < rows[r].tile_end; ++t) tile_rows[t] = (uint32_t)r;
+    void *drows, *dtiles;
+    memset(m, 0, N * 2);
+    memset(v, 0, N * 2);
+    fill(p, N, 0.02f);
+    if (check_hip(hipMalloc(&drows, sizeof rows), "hipMalloc rows") ||
+        check_hip(hipMalloc(&dtiles, tiles * sizeof(uint32_t)), "hipMalloc tiles") ||
+        check_hip(hipMemcpy(drows, rows, sizeof rows, hipMemcpyHostToDevice), "copy rows") ||
+        check_hip(hipMemcpy(dtiles, tile_rows, tiles * sizeof(uint32_t), hipMemcpyHostToDevice), "copy tiles") ||
+        check_hip(hipMemcpy(dp, p, N * 4, hipMemcpyHostToDevice), "copy p") ||
+        check_hip(hipMemcpy(dm, m, N * 2, hipMemcpyHostToDevice), "copy m") ||
+        check_hip(hipMemcpy(dv, v, N * 2, hipMemcpyHostToDevice), "copy v"))
+      return 1;
+    const uint64_t seed = 0x123456789ull, rng_step = 4;
+    if (check_rc(sr_adamw_multi((const sr_row*)drows, (const uint32_t*)dtiles, NULL, 3, tiles, SR_F32, SR_F32,
+                                SR_BF16, SR_STOCHASTIC, SR_BF16, SR_STOCHASTIC, &hp, seed, rng_step, block, NULL),
+                 "sr_adamw_multi"))
+      return 1;
+    for (int r = 0; r < 3; ++r) {
+      const uint32_t row_key = sr_update_key(seed, rng_step, param_index[r]);
+      oc_adamw(p + starts[r], 0, g + starts[r], 0, (uint16_t*)m + starts[r], 1, 1, (uint16_t*)v + starts[r], 1, 1,
+               sizes[r], hp_array, row_key, shard_start[r]);
+    }
+    if (check_hip(hipMemcpy(host, dp, N * 4, hipMemcpyDeviceToHost), "copy p")) return 1;
+    if (same(host, p, N * 4, "sr_adamw_multi parameters (3 rows and untouched gaps)")) return 1;
+    if (check_hip(hipMemcpy(host, dm, N * 2, hipMemcpyDeviceToHost), "copy m")) return 1;
+    if (same(host, m, N * 2, "sr_adamw_multi exp_avg")) return 1;
+    if (check_hip(hipMemcpy(host, dv, N * 2, hipMemcpyDeviceToHost), "copy v")) return 1;
+    if (same(host, v, N * 2, "sr_adamw_multi exp_avg_sq")) return 1;
+    hipFree(drows);
+    hipFree(dtiles);
+    free(tile_rows);
+  }
 
   /* Errors come back as codes with a message; nothing is launched. */
   if (sr_cast(dx, dy, N, 9, SR_NEAREST, 0u, 0u, 256, NULL) != SR_ERR_ARGUMENT || strlen(sr_last_error()) == 0) {

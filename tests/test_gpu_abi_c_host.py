@@ -1,8 +1,8 @@
 """The C ABI driven from plain C: no Python, no torch in the process.
 
 tests/native/abi_c_host.c allocates device memory with the HIP runtime,
-calls sr_cast, sr_adamw_step and sr_sgdm_step as a C, Go (cgo) or Rust host
-would, and compares every output byte with the C oracle linked into it; it
+calls sr_cast, sr_adamw_step, sr_sgdm_step and sr_adamw_multi (with the row
+table and tile map it builds) as a C, Go (cgo) or Rust host would, and compares every output byte with the C oracle linked into it; it
 also checks that a bad argument comes back as SR_ERR_ARGUMENT with a message.
 """
 
@@ -24,4 +24,4 @@ def test_plain_c_host_matches_the_c_oracle(cuda):
     assert result.returncode == 0, result.stdout + result.stderr
     lines = result.stdout.splitlines()
     assert lines[-1] == "abi_c_host ok"
-    assert sum(line.startswith("ok ") for line in lines) == 9, result.stdout
+    assert sum(line.startswith("ok ") for line in lines) == 12, result.stdout
