@@ -114,3 +114,17 @@ def test_lane_width_of_every_optimizer_launch():
             assert lib.sr_lane_elements(p, g, a, b) == _lib.LANE_ELEMENTS, (p, g, a, b)
     assert lib.sr_lane_elements(0, 0, 5, 0) == 0 and lib.sr_lane_elements(-1, 0, 0, 0) == 0
     assert _lib.lane_elements(torch.float32, torch.float32, torch.float8_e4m3fn, torch.bfloat16) == 4
+
+
+@pytest.mark.parametrize("compiler,flags", [("gcc", ["-std=c99", "-x", "c"]), ("g++", ["-std=c++11", "-x", "c++"])])
+def test_header_is_strict_c99_and_cxx11(tmp_path, compiler, flags):
+    """include/sr_states_hip.h compiles warning-free, pedantic, with nothing but <stdint.h>."""
+    import subprocess
+    from pathlib import Path
+
+    include = Path(__file__).resolve().parents[1] / "include"
+    source = tmp_path / "use_header.c"
+    source.write_text('#include "sr_states_hip.h"\n'
+                      "int main(void) { sr_row r = {{0}}; (void)r; return sr_abi_version() == SR_ABI_VERSION ? 0 : 1; }\n")
+    subprocess.run([compiler, *flags, "-Wall", "-Wextra", "-Werror", "-pedantic", "-I", str(include), "-c",
+                    str(source), "-o", str(tmp_path / "use_header.o")], check=True)
