@@ -125,6 +125,6 @@ def test_header_is_strict_c99_and_cxx11(tmp_path, compiler, flags):
     include = Path(__file__).resolve().parents[1] / "include"
     source = tmp_path / "use_header.c"
     source.write_text('#include "sr_states_hip.h"\n'
-                      "int main(void) { sr_row r = {{0}}; (void)r; return sr_abi_version() == SR_ABI_VERSION ? 0 : 1; }\n")
+                      "int main(void) { sr_row r; r.numel = 1; return r.numel == 1 && sr_abi_version() == SR_ABI_VERSION ? 0 : 1; }\n")
     subprocess.run([compiler, *flags, "-Wall", "-Wextra", "-Werror", "-pedantic", "-I", str(include), "-c",
                     str(source), "-o", str(tmp_path / "use_header.o")], check=True)
