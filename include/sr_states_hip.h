@@ -74,7 +74,7 @@ enum sr_error {
 /* One parameter of a multi-tensor bucket (64 bytes, device memory).
  * Together with a per-tile row map (uint32 row index per tile) it replaces
  * the reference's tables `meta`, `chunks` and `pointers`
- * (sr_states/triton/_multi_tensor.py:146-239, consumed by
+ * (built by sr_states/triton/_multi_tensor.py:43-47, 64-134, consumed by
  * sr_states/triton/_common.py:47-60). */
 typedef struct sr_row {
   uint64_t ptr[4];      /* parameter, gradient, state 0, state 1 (0 for SGDM) */
@@ -142,7 +142,7 @@ uint32_t sr_state_key(uint32_t key, uint32_t state_index);
 /* y[i] = round(x[i]) for i < n, counter = i + seed + offset (mod 2^32).
  * x: contiguous FP32; y: contiguous storage of `dtype`; x and y disjoint.
  * Replaces the `_cast_kernel` launch of sr_states/triton/cast.py:47-60 and
- * `_sr_cast_bf16_kernel` of sr_states/triton/sr_cast.py:191-224; its
+ * `_sr_cast_bf16_kernel` of sr_states/triton/sr_cast.py:55-86, 131-164; its
  * arithmetic is sr_states/rounding.py:97-142. */
 int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule,
             uint32_t seed, uint32_t offset, int block_size, void* stream);
@@ -151,7 +151,8 @@ int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule,
 
 /* One tensor.  p, g: FP32 or BF16; m, v: any sr_dtype.  `key` is the
  * parameter's update key; `offset` the flat shard start.
- * Replaces `_fused_adamw_kernel` (sr_states/triton/adamw.py:160-221). */
+ * Replaces `_fused_adamw_kernel` (sr_states/triton/adamw.py:59-100) and its
+ * launch by `triton_adamw_step_` (sr_states/triton/adamw.py:160-221). */
 int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n,
                   int p_dtype, int g_dtype, int m_dtype, int m_rule,
                   int v_dtype, int v_rule, const sr_adamw_hparams* hp,
@@ -186,7 +187,8 @@ int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, const float* r
 
 /* ---- fused momentum SGD ----------------------------------------------- */
 
-/* Replaces `_fused_sgdm_kernel` (sr_states/triton/sgd.py:434-490). */
+/* Replaces `_fused_sgdm_kernel` (sr_states/triton/sgd.py:47-72) and its launch
+ * by `triton_sgdm_step_` (sr_states/triton/sgd.py:115-171). */
 int sr_sgdm_step(void* p, const void* g, void* u, int64_t n,
                  int p_dtype, int g_dtype, int u_dtype, int u_rule,
                  const sr_sgdm_hparams* hp, uint32_t key, uint32_t offset,
@@ -195,7 +197,7 @@ int sr_sgdm_step(void* p, const void* g, void* u, int64_t n,
 /* Same table layout as sr_adamw_multi (state 1 pointer unused); tiles are
  * block_size * sr_lane_elements(p_dtype, g_dtype, u_dtype, u_dtype) elements.
  * Replaces `_multi_sgdm_kernel` and its launch
- * (sr_states/triton/sgd.py:393-431, 533-556). */
+ * (sr_states/triton/sgd.py:74-112, 214-237). */
 int sr_sgdm_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint32_t total_tiles,
                   int p_dtype, int g_dtype, int u_dtype, int u_rule,
                   const sr_sgdm_hparams* hp, uint64_t seed, uint64_t rng_step,

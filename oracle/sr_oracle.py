@@ -201,7 +201,8 @@ def cast(x: torch.Tensor, *, dtype, rounding="stochastic", seed=0, offset=0) -> 
 
 
 # ---------------------------------------------------------------------------
-# Functional recurrences (sr_states/reference/adamw.py:54-105, sgd.py:44-72)
+# Functional recurrences (sr_states/reference/adamw.py:54-105,
+# sr_states/reference/sgd.py:44-72)
 # ---------------------------------------------------------------------------
 
 
@@ -233,17 +234,6 @@ def adamw_step(p, g, m, v, *, lr, beta1, beta2, eps, weight_decay, step, formats
         for i, (value, fmt) in enumerate(zip((m32, v32), formats))
     ]
     return new_p.to(p.dtype), stored[0], stored[1]
-
-
-def adamw_proposals(p, g, m, v, *, lr, beta1, beta2, eps, weight_decay, step):
-    """The FP32 values adamw_step rounds: (p', m', v') before storage."""
-    p32, g32 = p.float(), g.float()
-    m32 = m.float().mul(beta1).add(g32, alpha=1.0 - beta1)
-    v32 = v.float().mul(beta2).addcmul(g32, g32, value=1.0 - beta2)
-    denominator = v32.sqrt().div_((1.0 - beta2**step) ** 0.5).add_(eps)
-    new_p = p32.mul(1.0 - lr * weight_decay)
-    new_p.addcdiv_(m32, denominator, value=-lr / (1.0 - beta1**step))
-    return new_p, m32, v32
 
 
 def sgdm_step(p, g, u, *, lr, momentum_factor, formats, seed, offset=0):

@@ -34,9 +34,7 @@ def native_cast(x, *, dtype, rule, seed=0, offset=0, threads=_DEFAULT_THREADS, o
     if out is None:
         output = torch.empty(x.shape, dtype=dtype, device=x.device)
     else:
-        if out.dtype != dtype or out.shape != x.shape or out.device != x.device or not out.is_contiguous():
-            raise ValueError("out must be a contiguous tensor of the requested dtype, shape and device")
-        output = out
+        output = check_out(x, out, dtype)
     if x.numel():
         with torch.cuda.device(x.device):
             _lib.call(
@@ -52,6 +50,21 @@ def native_cast(x, *, dtype, rule, seed=0, offset=0, threads=_DEFAULT_THREADS, o
                 _lib.stream_handle(x.device),
             )
     return output
+
+
+def check_out(x, out, dtype):
+    """``out`` for a cast of ``x`` to ``dtype``: contiguous, same shape and device, disjoint.
+
+    Workgroups read x and write out concurrently, so any shared byte would
+    make the result depend on their timing.
+    """
+    if out.dtype != dtype or out.shape != x.shape or out.device != x.device or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of the requested dtype, shape and device")
+    if x.numel():
+        x_start, out_start = x.data_ptr(), out.data_ptr()
+        if x_start < out_start + out.nbytes and out_start < x_start + x.nbytes:
+            raise ValueError("out must not overlap the input")
+    return out
 
 
 def _launch_shape(block_size, num_warps):
@@ -81,12 +94,12 @@ def cast(x, *, dtype, rounding="stochastic", seed=0, offset=0, block_size=256, n
 
 
 def sr_cast_bf16(x, *, seed, offset=0, block_size=256, num_warps=4, store_mode="convert"):
-    """Stochastically cast contiguous GPU FP32 input to BF16 (triton/sr_cast.py:149-174)."""
+    """Stochastically cast contiguous GPU FP32 input to BF16 (triton/sr_cast.py:89-115)."""
     return _cast_bf16(x, seed, offset, block_size, num_warps, store_mode, _lib.SR_STOCHASTIC)
 
 
 def rn_cast_bf16(x, *, block_size=256, num_warps=4):
-    """Round to nearest, ties to even, through the same launch path (sr_cast.py:177-188)."""
+    """Round to nearest, ties to even, through the same launch path (triton/sr_cast.py:117-128)."""
     return _cast_bf16(x, 0, 0, block_size, num_warps, "convert", _lib.SR_NEAREST)
 
 

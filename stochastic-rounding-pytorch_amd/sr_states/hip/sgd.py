@@ -51,7 +51,7 @@ def hip_sgdm_step_(
     formats: tuple | dict | None = None,
     block_size: int = DEFAULT_BLOCK_SIZE,
 ) -> None:
-    """Apply one fused momentum-SGD update in place (triton/sgd.py:434-490).
+    """Apply one fused momentum-SGD update in place (triton/sgd.py:115-171).
 
     ``parameter``, ``gradient`` and ``momentum`` are same-shaped contiguous
     GPU tensors; parameter and gradient are FP32 or BF16 and the momentum uses
@@ -98,7 +98,7 @@ class SGDMHip(StateOptimizer):
     """Fused momentum SGD; BF16 stochastic momentum storage by default.
 
     Same arguments, group keys and checkpoint layout as ``SGDMTriton``
-    (triton/sgd.py:493-556).  There is no Nesterov, dampening or weight decay
+    (triton/sgd.py:174-237).  There is no Nesterov, dampening or weight decay
     option, as in the reference.
     """
 

@@ -150,6 +150,18 @@ def test_c4_mixed_fp8_saturation(cuda):
     assert any(bool((g.abs() == 5000).any()) for _, _, _, _, g, _ in samples)
 
 
+def test_north_star_full_size(cuda):
+    """The headline workload bench.py times: BF16-SR m and v over the 1.55 G-element set, 2 steps."""
+    spec = bench.WORKLOADS["north_star"]
+    assert sum(math.prod(s) for s in spec["shapes"]) == 1_547_698_176
+    assert tuple(tuple(f) for f in spec["formats"]) == ((torch.bfloat16, "stochastic"),) * 2
+    params, opt, samples = _run_optimizer_config(cuda, "north_star", 2, tensors=6, chunks=4)
+    assert len(params) == 50 and len({index for index, *_ in samples}) == 6
+    for p in params:
+        for name in ("exp_avg", "exp_avg_sq"):
+            assert opt.state[p][name].dtype == torch.bfloat16
+
+
 def test_c4_literal_24_blocks(cuda):
     """Config 4 at its literal size: 4.99 G elements over 169 tensors, one step."""
     spec = bench.WORKLOADS["c4_fp8_24block"]

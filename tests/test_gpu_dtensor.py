@@ -1,12 +1,14 @@
-"""DTensor parameters on the device: every rank's update is its slice of the unsharded update.
+"""DTensor parameters on the device: every rank's update is the oracle's update of its slice.
 
 A model's parameters are updated unsharded (plain tensors) and, for every
 rank of several meshes, as DTensors holding that rank's shards.  Each local
-parameter, state and step must equal the matching flat range of the
-unsharded result, bit for bit: the random stream of an element depends only
-on its flat index in the whole parameter (the reference's flat-split
-property, tests/test_rng_streams.py:122-150, which its optimizers cannot use
-with DTensors, sr_states/optim/_state.py:148-152).
+parameter and state must equal, bit for bit, the C oracle's replay of the
+same steps over the matching flat range, with the range's first flat index
+as the counter offset: the random stream of an element depends only on its
+flat index in the whole parameter (the reference's flat-split property,
+tests/test_rng_streams.py:122-150, which its optimizers cannot use with
+DTensors, sr_states/optim/_state.py:148-152).  The unsharded run is held to
+the same oracle, and each shard also equals its slice of the unsharded run.
 
 Ranks are simulated in one process on cuda:0: each rank's DeviceMesh is
 built with ``_rank`` and no process group, so nothing is communicated; the
@@ -25,6 +27,7 @@ from torch.distributed.device_mesh import DeviceMesh  # noqa: E402
 from torch.distributed.tensor import DTensor, Replicate, Shard  # noqa: E402
 
 import sr_states  # noqa: E402
+from oracle import c_oracle  # noqa: E402
 from sr_states.optim._dtensor import shard_start  # noqa: E402
 
 pytestmark = pytest.mark.gpu
@@ -88,8 +91,34 @@ def _run(make, params, grads, wrap, checkpoint_after=None):
     return parameters, optimizer
 
 
-def _compare(full_params, full_opt, shard_params, shard_opt, names, what):
-    for index, (full, shard) in enumerate(zip(full_params, shard_params)):
+def _replay(oracle, params, grads, index, start, stop):
+    """The C oracle's STEPS updates of params[index]'s flat range [start, stop)."""
+    p = params[index].reshape(-1)[start:stop].cpu().clone()
+    states = [torch.zeros(stop - start, dtype=dtype) for dtype, _ in oracle["formats"]]
+    for step, step_grads in enumerate(grads, start=1):
+        g = step_grads[index].reshape(-1)[start:stop].cpu().clone()
+        key = sr_states.update_key(oracle["seed"], step, index)
+        oracle["update"](p, g, *states, step, key, start)
+    return p, states
+
+
+def _check_oracle(oracle, params, grads, index, start, local_p, local_states, label):
+    stop = start + local_p.numel()
+    if stop == start:
+        return
+    p, states = _replay(oracle, params, grads, index, start, stop)
+    assert_bits_or_nan(local_p.reshape(-1).cpu(), p, f"{label}: parameter against the oracle")
+    for k, (local, expected) in enumerate(zip(local_states, states)):
+        assert_bits_or_nan(local.reshape(-1).cpu(), expected, f"{label}: state {k} against the oracle")
+
+
+def _compare(full_params, full_opt, shard_params, shard_opt, names, what, oracle, params, grads, indices=None):
+    """Each shard against its slice of the unsharded run and against the oracle.
+
+    ``indices`` are the parameters' indices in ``params`` (default: their positions).
+    """
+    indices = range(len(shard_params)) if indices is None else indices
+    for index, full, shard in zip(indices, full_params, shard_params):
         start = shard_start(shard)
         local = shard.to_local().reshape(-1)
         stop = start + local.numel()
@@ -103,6 +132,27 @@ def _compare(full_params, full_opt, shard_params, shard_opt, names, what):
             assert_bits_or_nan(stored.to_local().reshape(-1), full_state[name].reshape(-1)[start:stop],
                                f"{label}: {name}")
         assert shard_state.get("step") == full_state.get("step")
+        _check_oracle(oracle, params, grads, index, start, local,
+                      [shard_state[name].to_local() for name in names], label)
+
+
+def _check_unsharded(full_params, full_opt, names, oracle, params, grads, what):
+    for index, full in enumerate(full_params):
+        _check_oracle(oracle, params, grads, index, 0, full.detach(),
+                      [full_opt.state[full][name] for name in names], f"{what}, unsharded parameter {index}")
+
+
+def _adamw_oracle(seed, formats):
+    def update(p, g, m, v, step, key, offset):
+        c_oracle.adamw_step_(p, g, m, v, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01,
+                             step=step, formats=formats, seed=key, offset=offset)
+    return {"seed": seed, "formats": formats, "update": update}
+
+
+def _sgdm_oracle(seed, formats):
+    def update(p, g, u, step, key, offset):
+        c_oracle.sgdm_step_(p, g, u, lr=0.1, momentum_factor=0.9, formats=formats, seed=key, offset=offset)
+    return {"seed": seed, "formats": formats, "update": update}
 
 
 def _adamw_bf16_sr(parameters):
@@ -120,9 +170,11 @@ def _sgdm_fp16_sr(parameters):
 
 
 OPTIMIZERS = {
-    "adamw_bf16_sr": (_adamw_bf16_sr, ("exp_avg", "exp_avg_sq")),
-    "adamw_e4m3_bf16": (_adamw_e4m3_bf16, ("exp_avg", "exp_avg_sq")),
-    "sgdm_fp16_sr": (_sgdm_fp16_sr, ("momentum_buffer",)),
+    "adamw_bf16_sr": (_adamw_bf16_sr, ("exp_avg", "exp_avg_sq"),
+                      _adamw_oracle(11, [(torch.bfloat16, "stochastic")] * 2)),
+    "adamw_e4m3_bf16": (_adamw_e4m3_bf16, ("exp_avg", "exp_avg_sq"),
+                        _adamw_oracle(12, [(torch.float8_e4m3fn, "stochastic"), (torch.bfloat16, "stochastic")])),
+    "sgdm_fp16_sr": (_sgdm_fp16_sr, ("momentum_buffer",), _sgdm_oracle(13, [(torch.float16, "stochastic")])),
 }
 
 
@@ -130,15 +182,18 @@ OPTIMIZERS = {
 @pytest.mark.parametrize("kind", list(OPTIMIZERS))
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_fused_optimizers_update_each_shard_as_its_slice_of_the_whole(cuda, kind, mesh_shape, placements, dtype):
-    make, names = OPTIMIZERS[kind]
+    make, names, oracle = OPTIMIZERS[kind]
     params, grads = _problem(cuda, seed=len(kind) + len(mesh_shape), dtype=dtype)
     full_params, full_opt = _run(make, params, grads, lambda t: t.clone())
+    torch.cuda.synchronize()
+    _check_unsharded(full_params, full_opt, names, oracle, params, grads, kind)
     for rank in range(int(np.prod(mesh_shape))):
         mesh = _mesh(mesh_shape, rank)
         shard_params, shard_opt = _run(make, params, grads, lambda t: _shard(t, mesh, placements),
                                        checkpoint_after=2)
         torch.cuda.synchronize()
-        _compare(full_params, full_opt, shard_params, shard_opt, names, f"{kind} rank {rank}")
+        _compare(full_params, full_opt, shard_params, shard_opt, names, f"{kind} rank {rank}", oracle,
+                 params, grads)
 
 
 def test_per_parameter_path_updates_each_shard_as_its_slice_of_the_whole(cuda):
@@ -155,14 +210,25 @@ def test_per_parameter_path_updates_each_shard_as_its_slice_of_the_whole(cuda):
             buffer = states32[0] * 0.9 + g32
             return p32 - group["lr"] * torch.sign(buffer), (buffer,)
 
+    def update(p, g, u, step, key, offset):
+        # The same torch operations on the CPU, and the C oracle's cast.
+        buffer = u.float() * 0.9 + g
+        p.copy_(p - 0.01 * torch.sign(buffer))
+        u.copy_(c_oracle.cast(buffer, dtype=torch.bfloat16, rounding="stochastic",
+                              seed=sr_states.state_key(key, 0), offset=offset))
+
+    oracle = {"seed": 21, "formats": [(torch.bfloat16, "stochastic")], "update": update}
     params, grads = _problem(cuda, seed=3)
     full_params, full_opt = _run(SignMomentum, params, grads, lambda t: t.clone())
+    torch.cuda.synchronize()
+    _check_unsharded(full_params, full_opt, ("momentum_buffer",), oracle, params, grads, "sign momentum")
     mesh_shape, placements = (3,), (Shard(0),)
     for rank in range(3):
         mesh = _mesh(mesh_shape, rank)
         shard_params, shard_opt = _run(SignMomentum, params, grads, lambda t: _shard(t, mesh, placements))
         torch.cuda.synchronize()
-        _compare(full_params, full_opt, shard_params, shard_opt, ("momentum_buffer",), f"rank {rank}")
+        _compare(full_params, full_opt, shard_params, shard_opt, ("momentum_buffer",), f"rank {rank}", oracle,
+                 params, grads)
 
 
 def test_groups_mixing_dtensor_and_plain_parameters(cuda):
@@ -182,10 +248,14 @@ def test_groups_mixing_dtensor_and_plain_parameters(cuda):
                 parameter.grad = wrap(g)
             opt.step()
         torch.cuda.synchronize()
+        oracle, names = OPTIMIZERS["adamw_bf16_sr"][2], ("exp_avg", "exp_avg_sq")
         for k, (full, mixed) in enumerate(zip(full_params, parameters)):
             if k % 2 == 0:
-                _compare([full], full_opt, [mixed], opt, ("exp_avg", "exp_avg_sq"), f"rank {rank}")
+                _compare([full], full_opt, [mixed], opt, names, f"rank {rank}", oracle, params, grads,
+                         indices=[k])
             else:
                 assert_bits_or_nan(mixed.detach(), full.detach(), f"rank {rank}, plain parameter {k}")
-                for name in ("exp_avg", "exp_avg_sq"):
+                for name in names:
                     assert_bits_or_nan(opt.state[mixed][name], full_opt.state[full][name], f"{name} {k}")
+                _check_oracle(oracle, params, grads, k, 0, mixed.detach(),
+                              [opt.state[mixed][name] for name in names], f"rank {rank}, plain parameter {k}")

@@ -29,7 +29,7 @@ MODES = ("stochastic", "nearest")
                                    torch.float8_e5m2])
 @pytest.mark.parametrize("mode", MODES)
 def test_shorthand_single_and_dict_are_identical(cuda, kind, dtype, mode):
-    """tests/test_minifloat_gpu.py:166-187."""
+    """tests/test_minifloat_gpu.py:166-186."""
     import sr_states
     from sr_states import StateFormat
 

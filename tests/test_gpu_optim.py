@@ -163,7 +163,7 @@ def test_adamw_zero_gradient_and_decay(cuda, betas):
 
 
 def test_round_to_nearest_variants_store_deterministic_bf16_state(cuda):
-    """tests/test_reference_optimizers.py:90-104 on the device.
+    """tests/test_reference_optimizers.py:90-103 on the device.
 
     The RN classes store BF16 states rounded to nearest even: the first
     momentum equals the gradient converted by torch, and neither class's

@@ -150,6 +150,24 @@ def test_builtin_casts_never_run_on_the_cpu():
         sr_states.sr_cast_bf16(x, seed=1)
 
 
+def test_cast_output_must_not_overlap_the_input():
+    """native_cast(out=...) refuses an output sharing any byte with the input."""
+    from sr_states.hip.cast import check_out
+
+    storage = torch.zeros(64)
+    x = storage[:16]
+    check_out(x, torch.empty(16, dtype=torch.bfloat16), torch.bfloat16)  # disjoint
+    check_out(x, storage[16:24].view(torch.bfloat16), torch.bfloat16)  # adjacent
+    for out in (storage[:8].view(torch.bfloat16), storage[15:23].view(torch.bfloat16),
+                storage[10:14].view(torch.float8_e4m3fn)):
+        dtype = out.dtype
+        with pytest.raises(ValueError, match="overlap"):
+            check_out(x, out, dtype)
+    check_out(storage[:0], storage[:0].view(torch.bfloat16), torch.bfloat16)  # empty: nothing shared
+    with pytest.raises(ValueError, match="contiguous tensor"):
+        check_out(x, torch.empty(16, dtype=torch.float16), torch.bfloat16)
+
+
 @pytest.mark.parametrize("arch", ["gfx950:sramecc+:xnack-", "gfx950", "gfx942:sramecc+:xnack-", "gfx90a", "gfx1100"])
 def test_device_check_accepts_only_the_built_architecture(monkeypatch, arch):
     """tests/test_fp8_storage.py:88-108, with the gfx950 check in place of sm_89.

@@ -107,7 +107,7 @@ def test_sampled_update_keys_are_distinct():
 
 @pytest.mark.parametrize("value", [0, 1, 16, -1, 2**31, 2**63 + 7, 2**90 + 2**33 + 4])
 def test_seeds_and_steps_use_their_low_64_bits(value):
-    """tests/test_multi_tensor_tables.py:351-355: the kernel takes the low 64 bits."""
+    """tests/test_multi_tensor_tables.py:178-182: the kernel takes the low 64 bits."""
     import sr_states
 
     low = value % 2**64

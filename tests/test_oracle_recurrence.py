@@ -111,6 +111,37 @@ def test_fp8_tie_rounds_to_even_without_fusion(n):
     assert torch.equal(tensors[2].float(), signs * (6 / 512))
 
 
+def test_adamw_fp8_first_moment_tie_rounds_to_even():
+    """AdamW's analogue of the FP8 tie: m = 2^-9, g = 331/512, beta1 = 0.9.
+
+    The eager order fma(g, 1 - beta1, RN(m beta1)) is exactly the E4M3 tie
+    0.06640625 and stores the even 0.0625; the other association and the
+    unfused sum lie just above the tie and would store 0.0703125, so the
+    case tells the orders apart.
+    """
+    signs = torch.tensor([1.0, -1.0, 1.0])
+    m = (signs * 2.0**-9).to(torch.float8_e4m3fn)
+    g = signs * (331 / 512)
+    beta1 = torch.tensor(0.9, dtype=torch.float32)
+    one_minus = torch.tensor(1.0 - 0.9, dtype=torch.float32)
+    scaled = m.float() * beta1
+    eager = (g.double() * one_minus.double() + scaled.double()).float()  # one rounding: the FMA
+    assert torch.equal(eager, signs * 0.06640625)
+    other = (m.float().double() * beta1.double() + (g * one_minus).double()).float()
+    unfused = scaled + g * one_minus
+    for value in (other, unfused):
+        assert not torch.equal(value, eager)
+        assert torch.equal(value.to(torch.float8_e4m3fn).float(), signs * 0.0703125)
+    options = {"lr": 1e-3, "beta1": 0.9, "beta2": 0.999, "eps": 1e-8, "weight_decay": 0.0, "step": 3}
+    formats = ((torch.float8_e4m3fn, "nearest"), (torch.bfloat16, "nearest"))
+    tensors = [torch.ones(3), g.clone(), m.clone(), torch.zeros(3, dtype=torch.bfloat16)]
+    reference = sr_oracle.adamw_step(*[t.clone() for t in tensors],
+                                     formats=tuple(sr_oracle.Fmt(*f) for f in formats), seed=9, **options)
+    assert torch.equal(reference[1].float(), signs * 0.0625)
+    c_oracle.adamw_step_(*tensors, formats=formats, seed=9, **options)
+    assert torch.equal(tensors[2].float(), signs * 0.0625)
+
+
 @pytest.mark.parametrize("kind", ["adamw", "sgdm"])
 def test_fp32_states_match_torch_optim(kind):
     initial = torch.linspace(-1, 1, 257)
