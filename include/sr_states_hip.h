@@ -185,6 +185,39 @@ int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, const float* r
                    int v_dtype, int v_rule, const sr_adamw_hparams* hp,
                    uint64_t seed, uint64_t rng_step, int block_size, void* stream);
 
+/* Limits of sr_adamw_multi_noalloc: its static device scratch holds this
+ * many rows and tiles (16.3 MiB per GPU). */
+#define SR_NOALLOC_MAX_ROWS 4096
+#define SR_NOALLOC_MAX_TILES (1u << 22)
+
+/* sr_adamw_multi without any device allocation by the caller or the library.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, hosts
+ * whose harness forbids hipMalloc).
+ *
+ * `rows` (nrows records) and `row_scalars` (NULL, or 2 * nrows floats as in
+ * sr_adamw_multi) are HOST memory.  The library checks them on the host
+ * (tile ranges that start at 0, follow each other and cover [0, total_tiles)
+ * with ceil(numel / T) tiles per row, non-null pointers, 16-byte alignment
+ * of vector rows, known flags, every correction2_sqrt in [2^-27, 1]), copies
+ * them into a static device array of the library, builds the tile-to-row map
+ * there with a small kernel, and launches the same kernel as sr_adamw_multi,
+ * all on `stream`.  Results equal sr_adamw_multi's for the same tables.
+ *
+ * Limits: 1 <= nrows <= SR_NOALLOC_MAX_ROWS and 1 <= total_tiles <=
+ * SR_NOALLOC_MAX_TILES (2^22 tiles: 2.1 G elements at 128-thread
+ * workgroups); larger buckets fail with SR_ERR_ARGUMENT before any device
+ * work.  The array is one per GPU and keeps the last call's contents: calls
+ * that overlap on one GPU (on different streams or threads) race, so a
+ * caller serializes them, for example on one stream.  The stream must belong
+ * to the current device.  Pageable `rows`/`row_scalars` may be reused when
+ * the call returns; pinned ones must stay unchanged until the stream has
+ * passed the call. */
+int sr_adamw_multi_noalloc(const sr_row* rows, const float* row_scalars, int nrows, uint32_t total_tiles,
+                           int p_dtype, int g_dtype, int m_dtype, int m_rule, int v_dtype, int v_rule,
+                           const sr_adamw_hparams* hp, uint64_t seed, uint64_t rng_step, int block_size,
+                           void* stream);
+
 /* ---- fused momentum SGD ----------------------------------------------- */
 
 /* Replaces `_fused_sgdm_kernel` (sr_states/triton/sgd.py:47-72) and its launch

@@ -8,6 +8,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/sr_states_hip.h"
@@ -112,6 +113,99 @@ sr::AdamWScalars adamw_scalars(const sr_adamw_hparams& h) {
 // correction2_sqrt in [2^-27, 1] (sr_math.h, div_by_constant); NaN fails.
 bool valid_correction(const sr_adamw_hparams& h) {
   return h.correction2_sqrt >= sr::kMinCorrection2Sqrt && h.correction2_sqrt <= 1.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the entry point that allocates nothing (sr_adamw_multi_noalloc).
+// One static device array per GPU holds the bucket's row records, its per-row
+// scalars and the tile-to-row map, in that order; each call overwrites the
+// parts it uses, so nothing needs clearing.  Calls that overlap on one GPU
+// share it and race.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchRowBytes = size_t{SR_NOALLOC_MAX_ROWS} * sizeof(sr_row);
+constexpr size_t kScratchScalarBytes = size_t{SR_NOALLOC_MAX_ROWS} * 2 * sizeof(float);
+constexpr size_t kScratchTileBytes = size_t{SR_NOALLOC_MAX_TILES} * sizeof(uint32_t);
+static_assert(kScratchRowBytes % 256 == 0 && kScratchScalarBytes % 256 == 0, "regions stay 256-byte aligned");
+
+static __device__ __align__(256) unsigned char scratch[kScratchRowBytes + kScratchScalarBytes + kScratchTileBytes];
+
+// Device address of `scratch` on each GPU, looked up once per device with
+// that device current.  The array's name in host code is only a handle for
+// the lookup, never an address to pass to a kernel or a copy.
+constexpr int kMaxDevices = 64;
+
+struct ScratchSlot {
+  std::once_flag once;
+  void* base = nullptr;
+  hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+int scratch_base(void* stream, unsigned char** base) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+  if (device < 0 || device >= kMaxDevices) return fail(SR_ERR_ARGUMENT, "device %d has no scratch slot", device);
+  if (stream) {
+    hipDevice_t owner = 0;
+    err = hipStreamGetDevice(static_cast<hipStream_t>(stream), &owner);
+    if (err != hipSuccess) return hip_fail(err, "hipStreamGetDevice");
+    if (owner != device)
+      return fail(SR_ERR_ARGUMENT, "stream belongs to device %d, but device %d is current", owner, device);
+  }
+  ScratchSlot& slot = g_scratch[device];
+  std::call_once(slot.once, [&slot] { slot.err = hipGetSymbolAddress(&slot.base, HIP_SYMBOL(scratch)); });
+  if (slot.err != hipSuccess) return hip_fail(slot.err, "hipGetSymbolAddress(scratch)");
+  *base = static_cast<unsigned char*>(slot.base);
+  return SR_OK;
+}
+
+// tile_rows[t] = the row whose tile range holds t, found by binary search
+// over the rows' first tiles (host-checked: they start at 0, increase and
+// cover [0, total_tiles) without gaps).  The threads of a wave hold
+// neighbouring tiles and mostly read the same records.
+constexpr int kFillBlock = 256;
+
+__global__ __launch_bounds__(kFillBlock) void fill_tile_rows(const sr_row* rows, int nrows, uint32_t* tile_rows,
+                                                             uint32_t total_tiles) {
+  const uint32_t t = blockIdx.x * kFillBlock + threadIdx.x;
+  if (t >= total_tiles) return;
+  int lo = 0, hi = nrows - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (rows[mid].tile_begin <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  tile_rows[t] = static_cast<uint32_t>(lo);
+}
+
+// The checks sr_adamw_multi leaves to its caller, made on the host copy.
+int check_host_rows(const sr_row* rows, const float* row_scalars, int nrows, uint32_t total_tiles,
+                    int64_t tile_elements) {
+  uint32_t next = 0;
+  for (int r = 0; r < nrows; ++r) {
+    const sr_row& row = rows[r];
+    if (row.numel < 1) return fail(SR_ERR_ARGUMENT, "row %d: numel %lld below 1", r, (long long)row.numel);
+    if (row.tile_begin != next) return fail(SR_ERR_ARGUMENT, "row %d: tiles start at %u, expected %u", r, row.tile_begin, next);
+    const int64_t tiles = (row.numel + tile_elements - 1) / tile_elements;
+    if (static_cast<int64_t>(row.tile_end) - row.tile_begin != tiles)
+      return fail(SR_ERR_ARGUMENT, "row %d: %u tiles for %lld elements, expected %lld", r,
+                  row.tile_end - row.tile_begin, (long long)row.numel, (long long)tiles);
+    if (row.flags & ~(SR_ROW_VECTOR | SR_ROW_KEYED)) return fail(SR_ERR_ARGUMENT, "row %d: unknown flags %#x", r, row.flags);
+    for (int k = 0; k < 4; ++k) {
+      if (!row.ptr[k]) return fail(SR_ERR_ARGUMENT, "row %d: null pointer %d", r, k);
+      if ((row.flags & SR_ROW_VECTOR) && (row.ptr[k] & 15u))
+        return fail(SR_ERR_ARGUMENT, "row %d: pointer %d not 16-byte aligned on a vector row", r, k);
+    }
+    if (row_scalars) {
+      const float c = row_scalars[2 * r + 1];
+      if (!(c >= sr::kMinCorrection2Sqrt && c <= 1.0f))
+        return fail(SR_ERR_ARGUMENT, "row %d: correction2_sqrt %g outside [2^-27, 1]", r, (double)c);
+    }
+    next = row.tile_end;
+  }
+  if (next != total_tiles) return fail(SR_ERR_ARGUMENT, "rows cover %u tiles, total_tiles is %u", next, total_tiles);
+  return SR_OK;
 }
 
 }  // namespace
@@ -270,6 +364,56 @@ int sr_sgdm_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint
                                        static_cast<uint32_t>(rng_step),
                                        static_cast<uint32_t>(rng_step >> 32));
   return launch(tables().sgdm[pi][gi][ue], block_size, total_tiles, &a, stream);
+}
+
+int sr_adamw_multi_noalloc(const sr_row* rows, const float* row_scalars, int nrows, uint32_t total_tiles,
+                           int p_dtype, int g_dtype, int m_dtype, int m_rule, int v_dtype, int v_rule,
+                           const sr_adamw_hparams* hp, uint64_t seed, uint64_t rng_step, int block_size,
+                           void* stream) {
+  const int pi = pg_index(p_dtype), gi = pg_index(g_dtype);
+  const int me = state_enc(m_dtype, m_rule), ve = state_enc(v_dtype, v_rule);
+  if (pi < 0 || gi < 0) return fail(SR_ERR_ARGUMENT, "parameter and gradient must be FP32 or BF16");
+  if (me < 0 || ve < 0) return fail(SR_ERR_ARGUMENT, "unsupported state dtype or rule");
+  if (!valid_block(block_size)) return fail(SR_ERR_ARGUMENT, "invalid block size %d", block_size);
+  if (!hp || !rows) return fail(SR_ERR_ARGUMENT, "null argument");
+  if (!valid_correction(*hp))
+    return fail(SR_ERR_ARGUMENT, "correction2_sqrt %g outside [2^-27, 1]", (double)hp->correction2_sqrt);
+  if (nrows < 1 || nrows > SR_NOALLOC_MAX_ROWS)
+    return fail(SR_ERR_ARGUMENT, "row count %d outside [1, %d] (the scratch holds %d rows)", nrows,
+                SR_NOALLOC_MAX_ROWS, SR_NOALLOC_MAX_ROWS);
+  if (total_tiles == 0 || total_tiles > SR_NOALLOC_MAX_TILES)
+    return fail(SR_ERR_ARGUMENT, "%u tiles outside [1, %u] (the scratch holds %u tiles)", total_tiles,
+                (unsigned)SR_NOALLOC_MAX_TILES, (unsigned)SR_NOALLOC_MAX_TILES);
+  const int64_t tile_elements =
+      static_cast<int64_t>(block_size) * sr::lane_elements(param_enc(pi), param_enc(gi), me, ve);
+  if (int rc = check_host_rows(rows, row_scalars, nrows, total_tiles, tile_elements)) return rc;
+  unsigned char* base = nullptr;
+  if (int rc = scratch_base(stream, &base)) return rc;
+  sr_row* rows_dev = reinterpret_cast<sr_row*>(base);
+  float* scalars_dev = reinterpret_cast<float*>(base + kScratchRowBytes);
+  uint32_t* tiles_dev = reinterpret_cast<uint32_t*>(base + kScratchRowBytes + kScratchScalarBytes);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err = hipMemcpyAsync(rows_dev, rows, sizeof(sr_row) * nrows, hipMemcpyHostToDevice, s);
+  if (err != hipSuccess) return hip_fail(err, "hipMemcpyAsync(rows)");
+  if (row_scalars) {
+    err = hipMemcpyAsync(scalars_dev, row_scalars, 2 * sizeof(float) * nrows, hipMemcpyHostToDevice, s);
+    if (err != hipSuccess) return hip_fail(err, "hipMemcpyAsync(row_scalars)");
+  }
+  const uint32_t fill_groups = (total_tiles + kFillBlock - 1) / kFillBlock;
+  hipLaunchKernelGGL(fill_tile_rows, dim3(fill_groups), dim3(kFillBlock), 0, s, rows_dev, nrows, tiles_dev,
+                     total_tiles);
+  err = hipGetLastError();
+  if (err != hipSuccess) return hip_fail(err, "fill_tile_rows launch");
+  sr::AdamWArgs a{};
+  a.rows = rows_dev;
+  a.tile_rows = tiles_dev;
+  a.row_scalars = row_scalars ? scalars_dev : nullptr;
+  a.total_tiles = total_tiles;
+  a.s = adamw_scalars(*hp);
+  a.key_prefix = sr::update_key_prefix(static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32),
+                                       static_cast<uint32_t>(rng_step),
+                                       static_cast<uint32_t>(rng_step >> 32));
+  return launch(tables().adamw[pi][gi][me][ve], block_size, total_tiles, &a, stream);
 }
 
 }  // extern "C"

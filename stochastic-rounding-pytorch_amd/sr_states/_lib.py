@@ -27,6 +27,8 @@ SR_F32, SR_BF16, SR_F16, SR_E4M3, SR_E5M2 = range(5)
 SR_NEAREST, SR_STOCHASTIC = 0, 1
 ROW_VECTOR = 1
 ROW_KEYED = 2
+# Scratch limits of sr_adamw_multi_noalloc (SR_NOALLOC_MAX_ROWS / _TILES).
+NOALLOC_MAX_ROWS, NOALLOC_MAX_TILES = 4096, 1 << 22
 
 DTYPE_CODES = {
     torch.float32: SR_F32,
@@ -94,6 +96,11 @@ SIGNATURES = {
     "sr_adamw_multi": (
         _int,
         [_vp, _vp, _vp, _int, _u32, _int, _int, _int, _int, _int, _int,
+         ctypes.POINTER(AdamWHparams), _u64, _u64, _int, _vp],
+    ),
+    "sr_adamw_multi_noalloc": (
+        _int,
+        [_vp, _vp, _int, _u32, _int, _int, _int, _int, _int, _int,
          ctypes.POINTER(AdamWHparams), _u64, _u64, _int, _vp],
     ),
     "sr_sgdm_step": (

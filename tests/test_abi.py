@@ -33,6 +33,7 @@ def test_header_declares_the_expected_surface():
             "sr_cast",
             "sr_adamw_step",
             "sr_adamw_multi",
+            "sr_adamw_multi_noalloc",
             "sr_sgdm_step",
             "sr_sgdm_multi",
         ]
@@ -90,6 +91,50 @@ def test_invalid_arguments_fail_before_any_device_work():
     sp = _lib.SgdmHparams()
     assert lib.sr_sgdm_multi(None, None, 0, 1, 0, 0, 7, 1, ctypes.byref(sp), 0, 0, 256, None) == 1
     assert b"unsupported state" in lib.sr_last_error()
+
+
+def test_noalloc_checks_its_host_tables_before_any_device_work():
+    """sr_adamw_multi_noalloc reads its tables on the host; bad ones never reach the GPU.
+
+    The pointers are fake addresses: nothing is dereferenced before the checks.
+    """
+    import numpy as np
+
+    from sr_states import _lib
+    from sr_states.hip._multi_tensor import build_records
+
+    lib = _lib.library()
+    hp = _lib.AdamWHparams(beta1=0.9, beta2=0.999, one_minus_beta1=0.1, one_minus_beta2=0.001,
+                           neg_step_size=-1e-3, correction2_sqrt=0.5, decay=1.0, eps=1e-8)
+    tile = 128 * _lib.LANE_ELEMENTS
+    pointers = [(0x10000, 0x20000, 0x30000, 0x40000), (0x50000, 0x60000, 0x70000, 0x80000)]
+    records = build_records([(4099, 0, 0), (600, 1, 0)], pointers, tile)
+    total = int(records["tile_end"][-1])
+
+    def status(table=records, nrows=2, tiles=total, scalars=None, block=128):
+        return lib.sr_adamw_multi_noalloc(table.ctypes.data, None if scalars is None else scalars.ctypes.data,
+                                          nrows, tiles, 0, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, block, None)
+
+    cases = [
+        (dict(nrows=_lib.NOALLOC_MAX_ROWS + 1), b"row count"),
+        (dict(tiles=_lib.NOALLOC_MAX_TILES + 1), b"tiles outside"),
+        (dict(tiles=0), b"tiles outside"),
+        (dict(tiles=total - 1), b"rows cover"),
+        (dict(block=256), b"tiles for"),
+        (dict(scalars=np.array([-1.0, 0.5, -1.0, 2.0], dtype=np.float32)), b"correction2_sqrt"),
+    ]
+    for kwargs, message in cases:
+        assert status(**kwargs) == 1, kwargs
+        assert message in lib.sr_last_error(), (kwargs, lib.sr_last_error())
+    negative = records.copy()
+    negative["numel"][0] = 0
+    assert status(negative) == 1 and b"numel 0 below 1" in lib.sr_last_error()
+    flagged = records.copy()
+    flagged["flags"][1] = 8
+    assert status(flagged) == 1 and b"unknown flags" in lib.sr_last_error()
+    assert lib.sr_adamw_multi_noalloc(None, None, 2, total, 0, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, 128,
+                                      None) == 1
+    assert b"null argument" in lib.sr_last_error()
 
 
 def test_call_raises_with_the_library_message():
