@@ -19,8 +19,10 @@ minimum reads+writes: parameter read+write, gradient read, each moment
 read+write, at their storage widths (20 B for FP32 p/g and BF16 moments).
 ``achieved`` = bytes per launch / mean kernel time: two HIP events on the
 launch stream bracket the K back-to-back steps (one launch per step).  A
-second pass of K steps, each between its own two events, gives
-``step_ms_median`` (and min, max); those events add about 2 us per step.
+second pass of K steps, each started on an idle GPU between its own two
+events, gives ``step_ms_median`` (and min, max; the events add about 2 us
+per step), ``host_ms_submit`` (median host time until step() returns) and
+``host_ms_wall`` (median host time until the step's work has finished).
 ``traffic`` comes from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
 measurement of the same workload, scaled by a copy-kernel calibration, when
 present.
@@ -33,7 +35,14 @@ this footprint.  ``frac`` there is the fused kernel's rate over it.
 
 cpu_baseline: the reference's eager CPU path (restated in oracle/sr_oracle.py
 with the same torch operations) timed on this host on a bounded sample of
-the same workload.
+the same workload.  ``validation``, in the same leg: sampled chunks of the
+timed workload's tensors, read before the first step and after the last,
+replayed through every step (warmup and both timed passes) by the C oracle
+and compared byte for byte; the run fails if any byte differs.
+
+``--workload bandwidth_matrix`` instead times trivial-math kernels that move
+subsets and rearrangements of the north star's streams at its footprint
+(tests/native/bandwidth_matrix.hip) and prints their rates.
 """
 
 from __future__ import annotations
@@ -42,6 +51,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -200,6 +210,20 @@ WORKLOADS = {
         hparams={},
         seed=0,
     ),
+    # Trivial-math stream variants at the north star's footprint
+    # (tests/native/bandwidth_matrix.hip): not an optimizer step.
+    "bandwidth_matrix": dict(
+        optimizer="matrix",
+        shapes=C4_BLOCK * 7 + [(32000, 4096)],
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=((torch.bfloat16, "stochastic"), (torch.bfloat16, "stochastic")),
+        grad_std=1.0,
+        hparams={},
+        seed=0,
+        steps=10,
+        warmup=3,
+    ),
     # Config 5: gradients with 5% exact zeros, 1% of magnitude below 2^-14
     # (FP16 subnormal range) and the rest N(0, 1e-2).
     "c5_sgdm_fp16": dict(
@@ -279,15 +303,25 @@ def make_optimizer(spec, device):
     return params, cls(params, state_format=formats, seed=spec["seed"], **spec["hparams"])
 
 
+class Workload:
+    """A built workload: its tensors, one step, and what validation reads back."""
+
+    def __init__(self, tensors, step, optimizer=None, casts=None):
+        self.tensors = tensors      # the tensors whose elements one step processes
+        self.step = step
+        self.optimizer = optimizer  # AdamWHip / SGDMHip of an optimizer workload
+        self.casts = casts          # (inputs, outputs) of a cast workload
+
+
 def build(spec, device):
-    """(tensors, step callable) of a workload, inputs resident on `device`."""
+    """The workload's inputs, resident on `device`, and its step."""
     import sr_states
 
     gen = torch.Generator(device=device).manual_seed(spec["seed"])
     if spec["optimizer"] == "copy":
         src = torch.empty(spec["shapes"][0], device=device).normal_(generator=gen)
         dst = torch.empty_like(src)
-        return [src], lambda: dst.copy_(src)
+        return Workload([src], lambda: dst.copy_(src))
     if spec["optimizer"] == "cast":
         from sr_states.hip.cast import native_cast
 
@@ -301,9 +335,120 @@ def build(spec, device):
             k = turn[0] = (turn[0] + 1) % len(inputs)
             native_cast(inputs[k], dtype=dtype, rule=code, seed=spec["seed"], out=outputs[k])
 
-        return inputs[:1], cast_step
+        return Workload(inputs[:1], cast_step, casts=(inputs, outputs))
     params, opt = make_optimizer(spec, device)
-    return params, opt.step
+    return Workload(params, opt.step, optimizer=opt)
+
+
+# Validation samples: chunks of this many elements (odd, so that chunk edges
+# fall inside the kernels' 4-element lane groups) at the head, the tail and
+# random interior starts of a few tensors.
+SAMPLE_CHUNK = 4099
+
+
+def _sample_chunks(numel, count, rng):
+    starts = {0, max(0, numel - SAMPLE_CHUNK)}
+    while len(starts) < min(count, max(1, numel // SAMPLE_CHUNK)):
+        starts.add(rng.randrange(0, max(1, numel - SAMPLE_CHUNK)))
+    return [(s, min(SAMPLE_CHUNK, numel - s)) for s in sorted(starts)]
+
+
+def snapshot_samples(spec, work, tensors=3, chunks=3):
+    """Host copies of sampled chunks of the inputs, taken before the first step.
+
+    Each entry is (tensor index, start, length, inputs): the parameter and
+    gradient chunks of an optimizer workload, or the input chunk of one of
+    the cast's buffer pairs.
+    """
+    import random
+
+    rng = random.Random(spec["seed"])
+    if spec["optimizer"] == "cast":
+        inputs, _ = work.casts
+        picks = [0, len(inputs) - 1]
+        return [(k, s, n, [inputs[k].view(-1)[s:s + n].cpu()])
+                for k in picks for s, n in _sample_chunks(inputs[k].numel(), chunks, rng)]
+    if spec["optimizer"] not in ("adamw", "sgdm"):
+        return None
+    params = work.tensors
+    picks = sorted({0, len(params) - 1, *rng.sample(range(len(params)), min(tensors, len(params)) - 1)})
+    samples = []
+    for index in picks:
+        p = params[index]
+        flat_p, flat_g = p.detach().view(-1), p.grad.view(-1)
+        for start, length in _sample_chunks(p.numel(), chunks, rng):
+            samples.append((index, start, length, [flat_p[start:start + length].cpu(),
+                                                   flat_g[start:start + length].cpu()]))
+    return samples
+
+
+def read_back(spec, work, samples):
+    """The device bytes of every sampled chunk after the last step."""
+    if samples is None:
+        return None
+    if spec["optimizer"] == "cast":
+        _, outputs = work.casts
+        return [[outputs[k].view(-1)[s:s + n].cpu()] for k, s, n, _ in samples]
+    opt, params = work.optimizer, work.tensors
+    finals = []
+    for index, start, length, _ in samples:
+        p = params[index]
+        values = [p.detach().view(-1)[start:start + length].cpu()]
+        values += [opt.state[p][name].view(-1)[start:start + length].cpu() for name in opt._state_names]
+        finals.append(values)
+    return finals
+
+
+def validate(spec, samples, finals, steps):
+    """Replay every step on the sampled chunks with the C oracle; compare bytes.
+
+    Each element's update depends only on its own inputs, its flat index and
+    its parameter's update key, so the oracle run on a chunk with ``offset``
+    set to the chunk's start must reproduce the device's bytes exactly (NaN
+    payloads aside), after all ``steps`` optimizer steps (warmup and timed).
+    """
+    sys.path.insert(0, str(ROOT))
+    from oracle import c_oracle, sr_oracle
+
+    def same(actual, expected):
+        a, e = actual.float(), expected.float()
+        nan = torch.isnan(e)
+        if not torch.equal(torch.isnan(a), nan):
+            return int((torch.isnan(a) != nan).sum())
+        bits = {4: torch.int32, 2: torch.int16, 1: torch.uint8}[actual.element_size()]
+        return int((actual.view(bits)[~nan] != expected.view(bits)[~nan]).sum())
+
+    mismatches = checked = 0
+    started = time.perf_counter()
+    for (index, start, length, inputs), final in zip(samples, finals):
+        if spec["optimizer"] == "cast":
+            (dtype, rule), = spec["formats"]
+            expected = [c_oracle.cast(inputs[0], dtype=dtype, rounding=rule, seed=spec["seed"], offset=start)]
+        else:
+            p, g = inputs[0].clone(), inputs[1]
+            states = [torch.zeros(length, dtype=dtype) for dtype, _ in spec["formats"]]
+            hp = spec["hparams"]
+            for t in range(1, steps + 1):
+                key = sr_oracle.update_key(spec["seed"], t, index)
+                if spec["optimizer"] == "adamw":
+                    c_oracle.adamw_step_(p, g, *states, lr=hp["lr"], beta1=hp["betas"][0], beta2=hp["betas"][1],
+                                         eps=hp["eps"], weight_decay=hp["weight_decay"], step=t,
+                                         formats=spec["formats"], seed=key, offset=start)
+                else:
+                    c_oracle.sgdm_step_(p, g, *states, lr=hp["lr"], momentum_factor=hp["momentum"],
+                                        formats=spec["formats"], seed=key, offset=start)
+            expected = [p, *states]
+        for actual, want in zip(final, expected):
+            mismatches += same(actual, want)
+            checked += want.numel()
+    return {
+        "oracle": "oracle/sr_oracle.c (C restatement, correctly rounded FP32)",
+        "steps_replayed": steps if spec["optimizer"] != "cast" else 1,
+        "chunks": len(samples),
+        "elements_checked": checked,
+        "mismatches": mismatches,
+        "seconds": round(time.perf_counter() - started, 2),
+    }
 
 
 def _median_step_seconds(opt, target_seconds: float, min_steps: int = 3) -> tuple[float, int]:
@@ -380,11 +525,11 @@ CEILING_LIBRARY = ROOT / "tests" / "native" / "libstream_ceiling.so"
 def pattern_ceiling(spec, elements: int, reps: int):
     """Rate of the trivial kernel with this workload's streams, or None where none applies.
 
-    Covers FP32-parameter AdamW and SGDM launches whose gradient and states
+    Covers AdamW and SGDM launches whose parameter, gradient and states
     match one of the probe's patterns, and the cast with its eight rotating
     buffer pairs (tests/native/stream_ceiling.hip).
     """
-    if spec["optimizer"] not in ("adamw", "sgdm", "cast") or spec["p_dtype"] != torch.float32:
+    if spec["optimizer"] not in ("adamw", "sgdm", "cast"):
         return None
     if not CEILING_LIBRARY.exists():
         return None
@@ -403,15 +548,46 @@ def pattern_ceiling(spec, elements: int, reps: int):
         widths = [size(spec["g_dtype"])] + [size(dt) for dt, _ in spec["formats"]]
         if len(widths) == 2:
             widths.append(0)
-        lib.sr_stream_ceiling.restype = ctypes.c_int
-        lib.sr_stream_ceiling.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                          ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
+        lib.sr_stream_ceiling_p.restype = ctypes.c_int
+        lib.sr_stream_ceiling_p.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
         n = elements // 512 * 512
-        rc = lib.sr_stream_ceiling(n, *widths, reps, ctypes.byref(ms))
+        rc = lib.sr_stream_ceiling_p(n, size(spec["p_dtype"]), *widths, reps, ctypes.byref(ms))
     if rc != 0:
         return None
     return {"achieved": bytes_per_element(spec) * n / ms.value / 1e6, "kernel_ms": ms.value,
             "elements": n, "kernel": "stream_ceiling.hip: same streams, trivial arithmetic"}
+
+
+MATRIX_LIBRARY = ROOT / "tests" / "native" / "libbandwidth_matrix.so"
+
+
+def bandwidth_matrix(elements: int, reps: int, rounds: int):
+    """Rates of every variant of tests/native/bandwidth_matrix.hip over `elements` elements."""
+    import ctypes
+
+    if not MATRIX_LIBRARY.exists():
+        raise SystemExit(f"{MATRIX_LIBRARY} is not built (tests/native/build_checks.py)")
+    lib = ctypes.CDLL(str(MATRIX_LIBRARY))
+    lib.sr_bandwidth_variants.restype = ctypes.c_int
+    lib.sr_bandwidth_variant.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int)]
+    lib.sr_bandwidth_matrix.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
+                                        ctypes.POINTER(ctypes.c_float), ctypes.c_int]
+    count = lib.sr_bandwidth_variants()
+    ms = (ctypes.c_float * (count * rounds))()
+    n = elements // 4096 * 4096
+    if lib.sr_bandwidth_matrix(n, reps, rounds, ms, count) != 0:
+        raise SystemExit("sr_bandwidth_matrix failed")
+    rows = []
+    for v in range(count):
+        name, width = ctypes.c_char_p(), ctypes.c_int()
+        lib.sr_bandwidth_variant(v, ctypes.byref(name), ctypes.byref(width))
+        times = [ms[r * count + v] for r in range(rounds)]
+        rows.append({"variant": name.value.decode(), "bytes_per_element": width.value,
+                     "best_gbps": width.value * n / min(times) / 1e6,
+                     "mean_gbps": width.value * n / statistics.mean(times) / 1e6,
+                     "ms": times})
+    return n, rows
 
 
 def load_traffic(workload: str):
@@ -467,8 +643,22 @@ def main():
     if args.steps is None:
         args.steps = spec.get("steps", 100)
     device = torch.device("cuda", 0)
-    params, step = build(spec, device)
-    elements = sum(p.numel() for p in params)
+    if spec["optimizer"] == "matrix":
+        n, rows = bandwidth_matrix(sum(math.prod(s) for s in spec["shapes"]), args.steps, args.warmup)
+        print(json.dumps({
+            "metric": "bandwidth of trivial-math stream variants at the north star's footprint, 1 MI355X",
+            "value": rows[0]["best_gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "higher_is_better": True, "vs_baseline": None, "dtype": "u32",
+            "data": "constant fill, XOR folds", "elements": n,
+            "note": "steps = launches per variant per round, warmup = interleaved rounds",
+            "peak": HBM_PEAK_GBPS, "matrix": rows}), flush=True)
+        return
+    work = build(spec, device)
+    step = work.step
+    elements = sum(t.numel() for t in work.tensors)
+    # Inputs of the sampled chunks, read before the first step, for the
+    # validation of the timed workload's bytes (cpu_baseline leg).
+    samples = None if args.no_cpu_baseline else snapshot_samples(spec, work)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -489,16 +679,30 @@ def main():
     # duration.  No events sit between the steps: on an 18 us cast they would
     # add about 2 us each.
     kernel_ms = ms_per_step
-    # Spread of single steps: a second pass of K steps, each between its own
-    # two events (which add about 2 us per step on the launch stream).
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for i in range(args.steps):
-        starts[i].record()
+    # Single steps: a second pass of K steps, each started on an idle GPU
+    # and timed three ways (benchmarks/bench_optimizer_steps.py:315-363):
+    # device time between two events on the launch stream (which add about
+    # 2 us), host time to submit the step (the call returning), and host wall
+    # time until the step's work has finished.
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    step_ms, submit_ms, wall_ms = [], [], []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        start.record()
+        began = time.perf_counter_ns()
         step()
-        ends[i].record()
-    torch.cuda.synchronize()
-    step_ms = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
+        returned = time.perf_counter_ns()
+        end.record()
+        end.synchronize()
+        finished = time.perf_counter_ns()
+        step_ms.append(start.elapsed_time(end))
+        submit_ms.append((returned - began) / 1e6)
+        wall_ms.append((finished - began) / 1e6)
+    step_ms.sort()
+    if not all(math.isfinite(v) and v > 0 for v in (*step_ms, *submit_ms, *wall_ms, total_ms)):
+        raise SystemExit("nonpositive or nonfinite step timing")
+    finals = read_back(spec, work, samples)
+    total_steps = args.warmup + 2 * args.steps
 
     bpe = bytes_per_element(spec)
     bytes_per_launch = bpe * elements
@@ -550,9 +754,12 @@ def main():
             "step_ms_max": step_ms[-1],
             "algorithmic_bytes_per_launch": bytes_per_launch,
         },
+        "host_ms_submit": statistics.median(submit_ms),
+        "host_ms_wall": statistics.median(wall_ms),
         "cpu_baseline": None,
+        "validation": None,
     }
-    del params, step
+    del work, step
     torch.cuda.empty_cache()
     if not args.no_ceiling:
         # Timed like the fused steps: back-to-back launches between two events.
@@ -562,7 +769,10 @@ def main():
         result["roofline"]["pattern_ceiling"] = ceiling
     if not args.no_cpu_baseline and spec["optimizer"] != "copy":
         result["cpu_baseline"] = cpu_baseline(spec, args.cpu_seconds)
+        result["validation"] = validate(spec, samples, finals, total_steps)
     print(json.dumps(result), flush=True)
+    if result["validation"] and result["validation"]["mismatches"]:
+        raise SystemExit(f"validation failed: {result['validation']}")
 
 
 if __name__ == "__main__":

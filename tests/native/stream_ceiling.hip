@@ -1,8 +1,8 @@
 // The bandwidth ceiling of a fused update's access pattern, measured.
 //
 // A kernel with trivial arithmetic (XORs) that moves exactly the
-// streams of one fused-update launch: an FP32 parameter read and written, a
-// gradient read, and one or two states read and written, with the product's
+// streams of one fused-update launch: a parameter (FP32 or BF16) read and
+// written, a gradient read, and one or two states read and written, with the product's
 // tile shape (128 lanes x 4 elements), its XCD-chunked tile order
 // (sr_tile_order.h) and its non-temporal accesses.  Whatever rate this
 // kernel reaches for n elements is what the memory system gives that access
@@ -54,9 +54,10 @@ __device__ __forceinline__ void store(void* base, uint64_t i, typename Access<BY
       w, reinterpret_cast<typename Access<BYTES>::type*>(static_cast<char*>(base) + i * BYTES));
 }
 
-// G, M, V: bytes per element of the gradient and the two states (V = 0: one
-// state).  Tile t covers elements [t * kTile, (t + 1) * kTile) < n.
-template <int G, int M, int V>
+// P, G, M, V: bytes per element of the parameter, the gradient and the two
+// states (V = 0: one state).  Tile t covers elements [t * kTile, (t + 1) *
+// kTile) < n.
+template <int P, int G, int M, int V>
 __global__ __launch_bounds__(kBlock) void streams(void* p, const void* g, void* m, void* v, uint32_t tiles) {
   const uint32_t t = sr::tile_of(blockIdx.y * gridDim.x + blockIdx.x, tiles);
   if (t >= tiles) return;
@@ -64,7 +65,7 @@ __global__ __launch_bounds__(kBlock) void streams(void* p, const void* g, void* 
   // Every load is issued before any store, as in the fused kernels: the
   // pointers may alias as far as the compiler knows, so a load placed after
   // a store would wait for it.
-  auto wp = load<4>(p, i);
+  auto wp = load<P>(p, i);
   auto wg = load<G>(g, i);
   auto wm = load<M>(m, i);
   typename Access<(V > 0 ? V : 1)>::type wv{};
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(kBlock) void streams(void* p, const void* g, void* 
   wp ^= h;
   wm ^= h;
   wv ^= h;
-  store<4>(p, i, wp);
+  store<P>(p, i, wp);
   store<M>(m, i, wm);
   if constexpr (V > 0) store<V>(v, i, wv);
 }
@@ -108,36 +109,43 @@ __global__ __launch_bounds__(kCastBlock) void cast_streams(const void* x, void* 
 
 typedef void (*Kernel)(void*, const void*, void*, void*, uint32_t);
 
-Kernel pick(int g, int m, int v) {
-  if (g == 4 && m == 2 && v == 2) return streams<4, 2, 2>;
-  if (g == 2 && m == 2 && v == 2) return streams<2, 2, 2>;
-  if (g == 4 && m == 1 && v == 2) return streams<4, 1, 2>;
-  if (g == 4 && m == 2 && v == 0) return streams<4, 2, 0>;
-  if (g == 4 && m == 4 && v == 4) return streams<4, 4, 4>;
-  if (g == 4 && m == 1 && v == 1) return streams<4, 1, 1>;
-  if (g == 4 && m == 4 && v == 0) return streams<4, 4, 0>;
-  if (g == 4 && m == 1 && v == 0) return streams<4, 1, 0>;
+Kernel pick(int p, int g, int m, int v) {
+  if (p == 4) {
+    if (g == 4 && m == 2 && v == 2) return streams<4, 4, 2, 2>;
+    if (g == 2 && m == 2 && v == 2) return streams<4, 2, 2, 2>;
+    if (g == 4 && m == 1 && v == 2) return streams<4, 4, 1, 2>;
+    if (g == 4 && m == 2 && v == 0) return streams<4, 4, 2, 0>;
+    if (g == 4 && m == 4 && v == 4) return streams<4, 4, 4, 4>;
+    if (g == 4 && m == 1 && v == 1) return streams<4, 4, 1, 1>;
+    if (g == 4 && m == 4 && v == 0) return streams<4, 4, 4, 0>;
+    if (g == 4 && m == 1 && v == 0) return streams<4, 4, 1, 0>;
+  } else if (p == 2) {
+    if (g == 2 && m == 2 && v == 2) return streams<2, 2, 2, 2>;
+    if (g == 2 && m == 1 && v == 2) return streams<2, 2, 1, 2>;
+    if (g == 2 && m == 2 && v == 0) return streams<2, 2, 2, 0>;
+  }
   return nullptr;
 }
 
 }  // namespace
 
 // Average milliseconds per launch of the trivial kernel over n elements with
-// a gradient of g_bytes and states of m_bytes and v_bytes per element
-// (v_bytes 0: one state), over `reps` launches after two untimed ones.
-// Supported patterns: (4,2,2), (2,2,2), (4,1,2), (4,2,0), (4,4,4), (4,1,1),
-// (4,4,0), (4,1,0).  n must be a
-// positive multiple of 512 with n / 512 <= 2^31 - 4096 (the fused
-// launches' tile limit); the grid is laid out as the fused launches lay it
-// out (sr::launch_shape).  Returns 0, or 1 for an
-// unsupported argument, 2 for a HIP error (buffers are freed either way).
-extern "C" int sr_stream_ceiling(uint64_t n, int g_bytes, int m_bytes, int v_bytes, int reps,
-                                 float* avg_ms) {
-  const Kernel kernel = pick(g_bytes, m_bytes, v_bytes);
+// a parameter of p_bytes, a gradient of g_bytes and states of m_bytes and
+// v_bytes per element (v_bytes 0: one state), over `reps` launches after two
+// untimed ones.  Supported (p, g, m, v) patterns: FP32 parameters with
+// (4,2,2), (2,2,2), (4,1,2), (4,2,0), (4,4,4), (4,1,1), (4,4,0), (4,1,0);
+// BF16 parameters with (2,2,2), (2,1,2), (2,2,0).  n must be a positive
+// multiple of 512 with n / 512 <= 2^31 - 4096 (the fused launches' tile
+// limit); the grid is laid out as the fused launches lay it out
+// (sr::launch_shape).  Returns 0, or 1 for an unsupported argument, 2 for a
+// HIP error (buffers are freed either way).
+extern "C" int sr_stream_ceiling_p(uint64_t n, int p_bytes, int g_bytes, int m_bytes, int v_bytes, int reps,
+                                   float* avg_ms) {
+  const Kernel kernel = pick(p_bytes, g_bytes, m_bytes, v_bytes);
   if (!kernel || n == 0 || n % kTile || n / kTile > 0x7FFFF000ull || reps < 1 || !avg_ms) return 1;
   const uint32_t tiles = static_cast<uint32_t>(n / kTile);
   const sr::LaunchShape shape = sr::launch_shape(tiles, kBlock);
-  const size_t bytes[4] = {n * 4, n * g_bytes, n * m_bytes, n * v_bytes};
+  const size_t bytes[4] = {n * p_bytes, n * g_bytes, n * m_bytes, n * v_bytes};
   void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
   hipEvent_t start = nullptr, stop = nullptr;
   int rc = 2;
@@ -172,6 +180,11 @@ extern "C" int sr_stream_ceiling(uint64_t n, int g_bytes, int m_bytes, int v_byt
   for (void* b : buf)
     if (b) (void)hipFree(b);
   return rc;
+}
+
+// sr_stream_ceiling_p with an FP32 parameter.
+extern "C" int sr_stream_ceiling(uint64_t n, int g_bytes, int m_bytes, int v_bytes, int reps, float* avg_ms) {
+  return sr_stream_ceiling_p(n, 4, g_bytes, m_bytes, v_bytes, reps, avg_ms);
 }
 
 // Average milliseconds per launch of the cast-pattern kernel over n FP32
