@@ -155,23 +155,16 @@ __device__ __forceinline__ void store_words(char* ptr, const uint32_t* w) {
   }
 }
 
-template <int ENC, int E>
-__device__ __forceinline__ void load_vec(const void* base, int64_t i, uint32_t (&raw)[E]) {
-  constexpr int W = enc_bytes(ENC), BYTES = E * W;
-  constexpr uint32_t mask = W == 4 ? 0xFFFFFFFFu : (1u << (8 * W)) - 1u;
-  uint32_t w[(BYTES + 3) / 4];
-  load_words<BYTES>(static_cast<const char*>(base) + i * W, w);
-#pragma unroll
-  for (int k = 0; k < E; ++k) raw[k] = (w[k * W / 4] >> (8 * ((k * W) % 4))) & mask;
+// The storage words of the group of four elements at index i (a multiple
+// of four, base 16-byte aligned), moved as one access.
+template <int ENC>
+__device__ __forceinline__ void load_group(const void* base, int64_t i, uint32_t (&words)[group_words(ENC)]) {
+  load_words<kGroup * enc_bytes(ENC)>(static_cast<const char*>(base) + i * enc_bytes(ENC), words);
 }
 
-template <int ENC, int E>
-__device__ __forceinline__ void store_vec(void* base, int64_t i, const uint32_t (&raw)[E]) {
-  constexpr int W = enc_bytes(ENC), BYTES = E * W;
-  uint32_t w[(BYTES + 3) / 4] = {};
-#pragma unroll
-  for (int k = 0; k < E; ++k) w[k * W / 4] |= raw[k] << (8 * ((k * W) % 4));
-  store_words<BYTES>(static_cast<char*>(base) + i * W, w);
+template <int ENC>
+__device__ __forceinline__ void store_group(void* base, int64_t i, const uint32_t (&words)[group_words(ENC)]) {
+  store_words<kGroup * enc_bytes(ENC)>(static_cast<char*>(base) + i * enc_bytes(ENC), words);
 }
 
 template <int ENC>
@@ -220,17 +213,22 @@ template <int PE, int GE, int ME, int VE>
 __device__ __forceinline__ void adamw_vector(char* p, const char* g, char* m, char* v, int64_t i,
                                              uint32_t cm, uint32_t cv, const AdamWScalars& s) {
   constexpr int E = lane_elements(PE, GE, ME, VE);
-  uint32_t rp[E], rg[E], rm[E], rv[E];
-  load_vec<PE>(p, i, rp);
-  load_vec<GE>(g, i, rg);
-  load_vec<ME>(m, i, rm);
-  load_vec<VE>(v, i, rv);
-  const uint32_t base = static_cast<uint32_t>(i);
+  static_assert(E == kGroup, "a lane's elements are one group");
+  uint32_t wp[group_words(PE)], wg[group_words(GE)], wm[group_words(ME)], wv[group_words(VE)];
+  load_group<PE>(p, i, wp);
+  load_group<GE>(g, i, wg);
+  load_group<ME>(m, i, wm);
+  load_group<VE>(v, i, wv);
+  float pf[E], gf[E], mf[E], vf[E];
+  decode_group<PE>(wp, pf);
+  decode_group<GE>(wg, gf);
+  decode_group<ME>(wm, mf);
+  decode_group<VE>(wv, vf);
   float mo[E], vo[E], root[E];
   bool tiny = false;
 #pragma unroll
   for (int k = 0; k < E; ++k) {
-    adamw_moments(decode<GE>(rg[k]), decode<ME>(rm[k]), decode<VE>(rv[k]), s, mo[k], vo[k]);
+    adamw_moments(gf[k], mf[k], vf[k], s, mo[k], vo[k]);
     root[k] = sqrt_rn_wide(vo[k]);
     tiny |= sqrt_needs_library(vo[k]);
   }
@@ -242,14 +240,14 @@ __device__ __forceinline__ void adamw_vector(char* p, const char* g, char* m, ch
     }
   }
 #pragma unroll
-  for (int k = 0; k < E; ++k) {
-    rp[k] = encode<PE>(adamw_parameter(decode<PE>(rp[k]), mo[k], root[k], s), 0);
-    rm[k] = encode<ME>(mo[k], cm + base + k);
-    rv[k] = encode<VE>(vo[k], cv + base + k);
-  }
-  store_vec<PE>(p, i, rp);
-  store_vec<ME>(m, i, rm);
-  store_vec<VE>(v, i, rv);
+  for (int k = 0; k < E; ++k) pf[k] = adamw_parameter(pf[k], mo[k], root[k], s);
+  const uint32_t base = static_cast<uint32_t>(i);
+  encode_group<PE>(pf, 0u, wp);
+  encode_group<ME>(mo, cm + base, wm);
+  encode_group<VE>(vo, cv + base, wv);
+  store_group<PE>(p, i, wp);
+  store_group<ME>(m, i, wm);
+  store_group<VE>(v, i, wv);
 }
 
 template <int PE, int GE, int ME, int VE>
@@ -306,20 +304,21 @@ template <int PE, int GE, int UE>
 __device__ __forceinline__ void sgdm_vector(char* p, const char* g, char* u, int64_t i, uint32_t cu,
                                             const SgdmScalars& s) {
   constexpr int E = lane_elements(PE, GE, UE, UE);
-  uint32_t rp[E], rg[E], ru[E];
-  load_vec<PE>(p, i, rp);
-  load_vec<GE>(g, i, rg);
-  load_vec<UE>(u, i, ru);
-  const uint32_t base = static_cast<uint32_t>(i);
+  static_assert(E == kGroup, "a lane's elements are one group");
+  uint32_t wp[group_words(PE)], wg[group_words(GE)], wu[group_words(UE)];
+  load_group<PE>(p, i, wp);
+  load_group<GE>(g, i, wg);
+  load_group<UE>(u, i, wu);
+  float pf[E], gf[E], uf[E];
+  decode_group<PE>(wp, pf);
+  decode_group<GE>(wg, gf);
+  decode_group<UE>(wu, uf);
 #pragma unroll
-  for (int k = 0; k < E; ++k) {
-    float po, uo;
-    sgdm_update(decode<PE>(rp[k]), decode<GE>(rg[k]), decode<UE>(ru[k]), s, po, uo);
-    rp[k] = encode<PE>(po, 0);
-    ru[k] = encode<UE>(uo, cu + base + k);
-  }
-  store_vec<PE>(p, i, rp);
-  store_vec<UE>(u, i, ru);
+  for (int k = 0; k < E; ++k) sgdm_update(pf[k], gf[k], uf[k], s, pf[k], uf[k]);
+  encode_group<PE>(pf, 0u, wp);
+  encode_group<UE>(uf, cu + static_cast<uint32_t>(i), wu);
+  store_group<PE>(p, i, wp);
+  store_group<UE>(u, i, wu);
 }
 
 template <int PE, int GE, int UE>
@@ -377,18 +376,21 @@ __global__ __launch_bounds__(kMaxBlock) void cast_kernel(const CastArgs a) {
   const uint32_t tile = blockDim.x * E;
   const int64_t start = static_cast<int64_t>(t) * tile;
   if (a.vector_ok && start + tile <= a.n) {
+    static_assert(G == kGroup, "cast groups are encoder groups");
     uint32_t r[E / G][G];
 #pragma unroll
     for (int k = 0; k < E / G; ++k) {
-      load_vec<ENC_F32>(a.x, start + static_cast<int64_t>(k * blockDim.x + threadIdx.x) * G, r[k]);
+      load_group<ENC_F32>(a.x, start + static_cast<int64_t>(k * blockDim.x + threadIdx.x) * G, r[k]);
     }
 #pragma unroll
     for (int k = 0; k < E / G; ++k) {
       const int64_t i = start + static_cast<int64_t>(k * blockDim.x + threadIdx.x) * G;
-      const uint32_t base = a.counter_base + static_cast<uint32_t>(i);
+      float x[G];
 #pragma unroll
-      for (int j = 0; j < G; ++j) r[k][j] = encode<ENC>(bits_f32(r[k][j]), base + j);
-      store_vec<ENC>(a.y, i, r[k]);
+      for (int j = 0; j < G; ++j) x[j] = bits_f32(r[k][j]);
+      uint32_t words[group_words(ENC)];
+      encode_group<ENC>(x, a.counter_base + static_cast<uint32_t>(i), words);
+      store_group<ENC>(a.y, i, words);
     }
   } else {
 #pragma unroll

@@ -13,6 +13,8 @@
 
 #include <stdint.h>
 
+#include <type_traits>
+
 #if defined(__HIPCC__)
 #include <hip/hip_runtime.h>
 #define SR_HD __host__ __device__ __forceinline__
@@ -408,6 +410,231 @@ SR_HD float decode(uint32_t v) {
   } else {
     return minifloat_decode<E5M2>(v);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Groups of four consecutive elements.
+//
+// The kernels' vector paths move four consecutive elements per lane as one
+// access, so they decode and encode whole storage words (element k of a
+// group at byte k * width, little-endian).  On the device two elements share
+// one hardware convert where gfx950 has a paired form: v_cvt_pk_f32_fp8 /
+// _bf8 to decode, v_cvt_pk_fp8_f32 / _bf8_f32, v_cvt_pk_f16_f32 and
+// v_cvt_pk_bf16_f32 to encode, and v_cvt_sr_bf16_f32 writing either half of
+// its destination.  The bits equal the single-element forms' for every
+// input in every position of a group (tests/native/minifloat_check.hip and
+// tests/native/bf16_sr_check.hip check both sides on the device); on the
+// host the groups are the single-element forms.
+// ---------------------------------------------------------------------------
+constexpr int kGroup = 4;
+
+// Storage words of one group of encoding ENC.
+constexpr int group_words(int enc) { return enc_bytes(enc) * kGroup / 4; }
+
+constexpr float pow2f(int e) {
+  float r = 1.0f;
+  for (; e > 0; --e) r *= 2.0f;
+  for (; e < 0; ++e) r *= 0.5f;
+  return r;
+}
+
+// Element codes (one per 32-bit lane) packed into storage words, and back.
+template <int ENC>
+SR_HD void pack_group(const uint32_t (&codes)[kGroup], uint32_t (&words)[group_words(ENC)]) {
+  constexpr int W = enc_bytes(ENC);
+#pragma unroll
+  for (int j = 0; j < group_words(ENC); ++j) words[j] = 0u;
+#pragma unroll
+  for (int k = 0; k < kGroup; ++k) words[k * W / 4] |= codes[k] << (8 * ((k * W) % 4));
+}
+
+template <int ENC>
+SR_HD void unpack_group(const uint32_t (&words)[group_words(ENC)], uint32_t (&codes)[kGroup]) {
+  constexpr int W = enc_bytes(ENC);
+  constexpr uint32_t mask = W == 4 ? 0xFFFFFFFFu : (1u << (8 * W)) - 1u;
+#pragma unroll
+  for (int k = 0; k < kGroup; ++k) codes[k] = (words[k * W / 4] >> (8 * ((k * W) % 4))) & mask;
+}
+
+// The value minifloat_bits<F, STOCH> rounds b to, as FP32 bits, for every b
+// that is not a NaN (NaN gives an unspecified value; callers treat NaN
+// groups apart).  Nearest: the clamped input, which the convert rounds.
+// Stochastic with D <= 23 dropped bits: the grid value of
+// minifloat_bits_fast.  Below F's smallest subnormal 2^(EMIN - M) (D >= 24):
+// that subnormal when (hash >> 8) < floor(|b| 2^(24 - EMIN + M)), else 0 --
+// the integer form's threshold sig >> (D - 24), here one exact product (a
+// power of two; the result is below 2^24) and a truncating convert.  Every
+// result is exactly representable in F (or, for FP16, at least 65536 and
+// taken to Inf by the convert).
+template <class F>
+constexpr uint32_t kSubnormalBits = static_cast<uint32_t>(127 + F::kEmin - F::kM) << 23;
+
+// `subnormal` is kSubnormalBits<F>, passed in so that a caller encoding
+// several elements holds the constant in one register.
+template <class F, bool STOCH>
+SR_HD uint32_t minifloat_grid_bits(uint32_t b, uint32_t hash, uint32_t subnormal = kSubnormalBits<F>) {
+  const uint32_t sign = b & 0x80000000u;
+  uint32_t a = b & 0x7FFFFFFFu;
+  if (F::kSat) a = a < F::kMaxBits ? a : F::kMaxBits;  // also maps +-Inf to +-max
+  if constexpr (!STOCH) {
+    (void)hash;
+    return a | sign;
+  } else {
+    constexpr float kScale = pow2f(24 - F::kEmin + F::kM);
+    uint32_t rounded;
+    if (a >= subnormal) {
+#if defined(__HIP_DEVICE_COMPILE__)
+      // Each branch keeps its skip, so a wave whose elements all take one
+      // side never issues the other (the compiler drops skips over short
+      // blocks; an asm statement, even an empty one, keeps them).
+      __asm__ volatile("");
+#endif
+      const int E = static_cast<int>(a >> 23);
+      const int s_below = E - (118 + F::kEmin - F::kM);
+      const int s = s_below < 9 + F::kM ? s_below : 9 + F::kM;
+      rounded = (a + (~hash >> s)) & ~(0xFFFFFFFFu >> s);
+    } else {
+#if defined(__HIP_DEVICE_COMPILE__)
+      __asm__ volatile("");
+#endif
+      const uint32_t threshold = static_cast<uint32_t>(bits_f32(a) * kScale);
+      rounded = (hash >> 8) < threshold ? subnormal : 0u;
+    }
+    return rounded | sign;
+  }
+}
+
+// Decodes one group of storage words of ENC.
+template <int ENC>
+SR_HD void decode_group(const uint32_t (&words)[group_words(ENC)], float (&x)[kGroup]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  if constexpr (ENC == ENC_E4M3_RN || ENC == ENC_E4M3_SR || ENC == ENC_E5M2_RN || ENC == ENC_E5M2_SR) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    constexpr bool kE4M3 = ENC == ENC_E4M3_RN || ENC == ENC_E4M3_SR;
+    const int w = static_cast<int>(words[0]);
+    const f2 lo = kE4M3 ? __builtin_amdgcn_cvt_pk_f32_fp8(w, false) : __builtin_amdgcn_cvt_pk_f32_bf8(w, false);
+    const f2 hi = kE4M3 ? __builtin_amdgcn_cvt_pk_f32_fp8(w, true) : __builtin_amdgcn_cvt_pk_f32_bf8(w, true);
+    x[0] = lo.x;
+    x[1] = lo.y;
+    x[2] = hi.x;
+    x[3] = hi.y;
+    return;
+  }
+#endif
+  uint32_t codes[kGroup];
+  unpack_group<ENC>(words, codes);
+#pragma unroll
+  for (int k = 0; k < kGroup; ++k) x[k] = decode<ENC>(codes[k]);
+}
+
+// Encodes one group of FP32 values (bits b) with the random words
+// hash[k] (ignored by nearest encodings) into storage words of ENC.
+template <int ENC>
+SR_HD void encode_group_with(const uint32_t (&b)[kGroup], const uint32_t (&hash)[kGroup],
+                             uint32_t (&words)[group_words(ENC)]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  if constexpr (ENC == ENC_F32) {
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) words[k] = b[k];
+  } else if constexpr (ENC == ENC_BF16_SR) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint32_t h0 = hash[2 * j], h1 = hash[2 * j + 1];
+      // As in bf16_sr: the empty asm keeps each shift a shift.
+      __asm__("" : "+v"(h0));
+      __asm__("" : "+v"(h1));
+      bf16x2 pair = __builtin_amdgcn_cvt_sr_bf16_f32(bf16x2{}, __builtin_bit_cast(float, b[2 * j]), h0 << 16, false);
+      pair = __builtin_amdgcn_cvt_sr_bf16_f32(pair, __builtin_bit_cast(float, b[2 * j + 1]), h1 << 16, true);
+      words[j] = __builtin_bit_cast(uint32_t, pair);
+    }
+  } else if constexpr (ENC == ENC_BF16_RN) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    float x[kGroup];
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      // NaN becomes the quiet NaN whose nearest BF16 is the reference's
+      // 0x7FC0; the empty asm keeps an FMA producing b from fusing with the
+      // convert.
+      uint32_t v = (b[k] & 0x7FFFFFFFu) > 0x7F800000u ? 0x7FC00000u : b[k];
+      __asm__("" : "+v"(v));
+      x[k] = __builtin_bit_cast(float, v);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const bf16x2 pair = {static_cast<__bf16>(x[2 * j]), static_cast<__bf16>(x[2 * j + 1])};
+      words[j] = __builtin_bit_cast(uint32_t, pair);
+    }
+  } else {
+    using F = typename std::conditional<ENC == ENC_F16_RN || ENC == ENC_F16_SR, F16,
+              typename std::conditional<ENC == ENC_E4M3_RN || ENC == ENC_E4M3_SR, E4M3, E5M2>::type>::type;
+    constexpr bool kStoch = enc_stochastic(ENC);
+    uint32_t grid[kGroup];
+    bool nan = false;
+    uint32_t subnormal = kSubnormalBits<F>;
+    __asm__("" : "+v"(subnormal));  // one register for the group's four selects
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) {
+      nan |= (b[k] & 0x7FFFFFFFu) > 0x7F800000u;
+      grid[k] = minifloat_grid_bits<F, kStoch>(b[k], hash[k], subnormal);
+      __asm__("" : "+v"(grid[k]));  // no fusing of an FMA into the convert
+    }
+    float g[kGroup];
+#pragma unroll
+    for (int k = 0; k < kGroup; ++k) g[k] = __builtin_bit_cast(float, grid[k]);
+    if constexpr (F::kWidth == 16) {
+      typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f16x2 pair = {static_cast<_Float16>(g[2 * j]), static_cast<_Float16>(g[2 * j + 1])};
+        words[j] = __builtin_bit_cast(uint32_t, pair);
+      }
+    } else if constexpr (F::kM == 3) {
+      int w = __builtin_amdgcn_cvt_pk_fp8_f32(g[0], g[1], 0, false);
+      words[0] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(g[2], g[3], w, true));
+    } else {
+      int w = __builtin_amdgcn_cvt_pk_bf8_f32(g[0], g[1], 0, false);
+      words[0] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(g[2], g[3], w, true));
+    }
+    if (nan) {
+      // A NaN anywhere in the group: every element through the single-element
+      // form (rare; whole waves skip it).
+      __asm__ volatile("");
+      uint32_t codes[kGroup];
+#pragma unroll
+      for (int k = 0; k < kGroup; ++k) codes[k] = minifloat_bits_fast<F, kStoch>(b[k], hash[k]);
+      pack_group<ENC>(codes, words);
+    }
+  }
+#else
+  uint32_t codes[kGroup];
+#pragma unroll
+  for (int k = 0; k < kGroup; ++k) {
+    if constexpr (ENC == ENC_F32) codes[k] = b[k];
+    else if constexpr (ENC == ENC_BF16_RN) codes[k] = bf16_rn_bits(b[k]);
+    else if constexpr (ENC == ENC_BF16_SR) codes[k] = bf16_sr_bits(b[k], hash[k]);
+    else if constexpr (ENC == ENC_F16_RN) codes[k] = minifloat_bits<F16, false>(b[k], 0u);
+    else if constexpr (ENC == ENC_F16_SR) codes[k] = minifloat_bits<F16, true>(b[k], hash[k]);
+    else if constexpr (ENC == ENC_E4M3_RN) codes[k] = minifloat_bits<E4M3, false>(b[k], 0u);
+    else if constexpr (ENC == ENC_E4M3_SR) codes[k] = minifloat_bits<E4M3, true>(b[k], hash[k]);
+    else if constexpr (ENC == ENC_E5M2_RN) codes[k] = minifloat_bits<E5M2, false>(b[k], 0u);
+    else codes[k] = minifloat_bits<E5M2, true>(b[k], hash[k]);
+  }
+  pack_group<ENC>(codes, words);
+#endif
+}
+
+// Encodes one group with counters counter0 + k: the hash of each counter
+// for stochastic encodings (sr_states/_hash.py:31-50), nothing for nearest.
+template <int ENC>
+SR_HD void encode_group(const float (&x)[kGroup], uint32_t counter0, uint32_t (&words)[group_words(ENC)]) {
+  uint32_t b[kGroup], hash[kGroup];
+#pragma unroll
+  for (int k = 0; k < kGroup; ++k) {
+    b[k] = f32_bits(x[k]);
+    hash[k] = enc_stochastic(ENC) ? h32(counter0 + static_cast<uint32_t>(k)) : 0u;
+  }
+  encode_group_with<ENC>(b, hash, words);
 }
 
 // ---------------------------------------------------------------------------

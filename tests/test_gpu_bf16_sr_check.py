@@ -46,3 +46,23 @@ def test_hardware_nearest_convert_matches_the_reference_rule_on_every_input(cuda
     assert check.sr_check_bf16_rn(counters) == 0
     assert counters[1] == 2**32
     assert counters[0] == 0, f"{counters[0]} of 2^32 inputs differ"
+
+
+def test_group_converts_match_the_reference_rules_in_every_position(cuda):
+    """The four-element BF16 forms of the kernels' vector paths (two elements per convert).
+
+    Every FP32 input at each position of a group, stochastic at its five random
+    values and nearest; the twelve upper halves' (low half, random) pairs at
+    each position.
+    """
+    import torch  # noqa: F401  (load the HIP runtime first)
+
+    assert LIBRARY.exists(), f"{LIBRARY} is not built (tests/native/build_checks.py)"
+    check = ctypes.CDLL(str(LIBRARY))
+    check.sr_check_bf16_groups.restype = ctypes.c_int
+    check.sr_check_bf16_groups.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
+    counters = (ctypes.c_ulonglong * 2)()
+    assert check.sr_check_bf16_groups(counters) == 0
+    mismatches, comparisons = counters[0], counters[1]
+    assert comparisons == 96 * 2**32 + 12 * 2**31 * 32
+    assert mismatches == 0, f"{mismatches} of {comparisons} comparisons differ"

@@ -38,3 +38,24 @@ def test_device_minifloat_codecs_match_the_integer_forms_exhaustively(cuda, name
     mismatches, comparisons = counters[0], counters[1]
     assert comparisons == 7 * 2**32 + 2**width
     assert mismatches == 0, f"{name}: {mismatches} of {comparisons} comparisons differ"
+
+
+@pytest.mark.parametrize("name,code,width", [("float16", 0, 16), ("float8_e4m3fn", 1, 8), ("float8_e5m2", 2, 8)])
+def test_device_group_codecs_match_the_integer_forms_in_every_position(cuda, name, code, width):
+    """The four-element forms of the kernels' vector paths (two elements per paired convert).
+
+    Every FP32 input at each position of a group, beside finite companions and
+    beside a NaN companion, nearest and stochastic at its six random values;
+    every encoding at each position through the group decoder.
+    """
+    import torch  # noqa: F401  (load the HIP runtime first)
+
+    assert LIBRARY.exists(), f"{LIBRARY} is not built (tests/native/build_checks.py)"
+    check = ctypes.CDLL(str(LIBRARY))
+    check.sr_check_minifloat_groups.restype = ctypes.c_int
+    check.sr_check_minifloat_groups.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_ulonglong)]
+    counters = (ctypes.c_ulonglong * 2)()
+    assert check.sr_check_minifloat_groups(code, counters) == 0
+    mismatches, comparisons = counters[0], counters[1]
+    assert comparisons == 144 * 2**32 + 16 * 2**width
+    assert mismatches == 0, f"{name}: {mismatches} of {comparisons} comparisons differ"
