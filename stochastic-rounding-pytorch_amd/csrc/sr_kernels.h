@@ -167,6 +167,19 @@ __device__ __forceinline__ void store_group(void* base, int64_t i, const uint32_
   store_words<kGroup * enc_bytes(ENC)>(static_cast<char*>(base) + i * enc_bytes(ENC), words);
 }
 
+// The same with a workgroup-uniform tile base and the lane's group index j
+// below 2^30: the address is a scalar base plus a 32-bit lane offset, which
+// the loads and stores take as such (no per-lane 64-bit address arithmetic).
+template <int ENC>
+__device__ __forceinline__ void load_lane_group(const char* tile, uint32_t j, uint32_t (&words)[group_words(ENC)]) {
+  load_words<kGroup * enc_bytes(ENC)>(tile + j * static_cast<uint32_t>(kGroup * enc_bytes(ENC)), words);
+}
+
+template <int ENC>
+__device__ __forceinline__ void store_lane_group(char* tile, uint32_t j, const uint32_t (&words)[group_words(ENC)]) {
+  store_words<kGroup * enc_bytes(ENC)>(tile + j * static_cast<uint32_t>(kGroup * enc_bytes(ENC)), words);
+}
+
 template <int ENC>
 __device__ __forceinline__ uint32_t load1(const void* base, int64_t i) {
   constexpr int W = enc_bytes(ENC);
@@ -209,16 +222,19 @@ __device__ __forceinline__ uint32_t row_key(const Args& a, const sr_row& r) {
 // ---------------------------------------------------------------------------
 // Fused AdamW.
 // ---------------------------------------------------------------------------
+// One lane's group of a full vector tile: p, g, m, v point at the tile's
+// first element (workgroup-uniform), j is the lane's group in the tile and
+// `index` the flat index (mod 2^32) of its first element.
 template <int PE, int GE, int ME, int VE>
-__device__ __forceinline__ void adamw_vector(char* p, const char* g, char* m, char* v, int64_t i,
-                                             uint32_t cm, uint32_t cv, const AdamWScalars& s) {
+__device__ __forceinline__ void adamw_vector(char* p, const char* g, char* m, char* v, uint32_t j,
+                                             uint32_t index, uint32_t cm, uint32_t cv, const AdamWScalars& s) {
   constexpr int E = lane_elements(PE, GE, ME, VE);
   static_assert(E == kGroup, "a lane's elements are one group");
   uint32_t wp[group_words(PE)], wg[group_words(GE)], wm[group_words(ME)], wv[group_words(VE)];
-  load_group<PE>(p, i, wp);
-  load_group<GE>(g, i, wg);
-  load_group<ME>(m, i, wm);
-  load_group<VE>(v, i, wv);
+  load_lane_group<PE>(p, j, wp);
+  load_lane_group<GE>(g, j, wg);
+  load_lane_group<ME>(m, j, wm);
+  load_lane_group<VE>(v, j, wv);
   float pf[E], gf[E], mf[E], vf[E];
   decode_group<PE>(wp, pf);
   decode_group<GE>(wg, gf);
@@ -241,13 +257,12 @@ __device__ __forceinline__ void adamw_vector(char* p, const char* g, char* m, ch
   }
 #pragma unroll
   for (int k = 0; k < E; ++k) pf[k] = adamw_parameter(pf[k], mo[k], root[k], s);
-  const uint32_t base = static_cast<uint32_t>(i);
   encode_group<PE>(pf, 0u, wp);
-  encode_group<ME>(mo, cm + base, wm);
-  encode_group<VE>(vo, cv + base, wv);
-  store_group<PE>(p, i, wp);
-  store_group<ME>(m, i, wm);
-  store_group<VE>(v, i, wv);
+  encode_group<ME>(mo, cm + index, wm);
+  encode_group<VE>(vo, cv + index, wv);
+  store_lane_group<PE>(p, j, wp);
+  store_lane_group<ME>(m, j, wm);
+  store_lane_group<VE>(v, j, wv);
 }
 
 template <int PE, int GE, int ME, int VE>
@@ -286,8 +301,9 @@ __global__ __launch_bounds__(kMaxBlock) void adamw_kernel(const AdamWArgs a) {
   const uint32_t tile = blockDim.x * E;
   const int64_t start = static_cast<int64_t>(t - r.tile_begin) * tile;
   if ((r.flags & SR_ROW_VECTOR) && start + tile <= numel) {
-    adamw_vector<PE, GE, ME, VE>(p, g, m, v, start + static_cast<int64_t>(threadIdx.x) * E, cm,
-                                 cv, s);
+    adamw_vector<PE, GE, ME, VE>(p + start * enc_bytes(PE), g + start * enc_bytes(GE), m + start * enc_bytes(ME),
+                                 v + start * enc_bytes(VE), threadIdx.x,
+                                 static_cast<uint32_t>(start) + threadIdx.x * E, cm, cv, s);
   } else {
 #pragma unroll
     for (int k = 0; k < E; ++k) {
@@ -300,15 +316,16 @@ __global__ __launch_bounds__(kMaxBlock) void adamw_kernel(const AdamWArgs a) {
 // ---------------------------------------------------------------------------
 // Fused momentum SGD.
 // ---------------------------------------------------------------------------
+// One lane's group of a full vector tile, as adamw_vector.
 template <int PE, int GE, int UE>
-__device__ __forceinline__ void sgdm_vector(char* p, const char* g, char* u, int64_t i, uint32_t cu,
-                                            const SgdmScalars& s) {
+__device__ __forceinline__ void sgdm_vector(char* p, const char* g, char* u, uint32_t j, uint32_t index,
+                                            uint32_t cu, const SgdmScalars& s) {
   constexpr int E = lane_elements(PE, GE, UE, UE);
   static_assert(E == kGroup, "a lane's elements are one group");
   uint32_t wp[group_words(PE)], wg[group_words(GE)], wu[group_words(UE)];
-  load_group<PE>(p, i, wp);
-  load_group<GE>(g, i, wg);
-  load_group<UE>(u, i, wu);
+  load_lane_group<PE>(p, j, wp);
+  load_lane_group<GE>(g, j, wg);
+  load_lane_group<UE>(u, j, wu);
   float pf[E], gf[E], uf[E];
   decode_group<PE>(wp, pf);
   decode_group<GE>(wg, gf);
@@ -316,9 +333,9 @@ __device__ __forceinline__ void sgdm_vector(char* p, const char* g, char* u, int
 #pragma unroll
   for (int k = 0; k < E; ++k) sgdm_update(pf[k], gf[k], uf[k], s, pf[k], uf[k]);
   encode_group<PE>(pf, 0u, wp);
-  encode_group<UE>(uf, cu + static_cast<uint32_t>(i), wu);
-  store_group<PE>(p, i, wp);
-  store_group<UE>(u, i, wu);
+  encode_group<UE>(uf, cu + index, wu);
+  store_lane_group<PE>(p, j, wp);
+  store_lane_group<UE>(u, j, wu);
 }
 
 template <int PE, int GE, int UE>
@@ -345,7 +362,8 @@ __global__ __launch_bounds__(kMaxBlock) void sgdm_kernel(const SgdmArgs a) {
   const uint32_t tile = blockDim.x * E;
   const int64_t start = static_cast<int64_t>(t - r.tile_begin) * tile;
   if ((r.flags & SR_ROW_VECTOR) && start + tile <= numel) {
-    sgdm_vector<PE, GE, UE>(p, g, u, start + static_cast<int64_t>(threadIdx.x) * E, cu, a.s);
+    sgdm_vector<PE, GE, UE>(p + start * enc_bytes(PE), g + start * enc_bytes(GE), u + start * enc_bytes(UE),
+                            threadIdx.x, static_cast<uint32_t>(start) + threadIdx.x * E, cu, a.s);
   } else {
 #pragma unroll
     for (int k = 0; k < E; ++k) {

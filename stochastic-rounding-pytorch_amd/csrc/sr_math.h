@@ -556,7 +556,8 @@ SR_HD void encode_group_with(const uint32_t (&b)[kGroup], const uint32_t (&hash)
       // NaN becomes the quiet NaN whose nearest BF16 is the reference's
       // 0x7FC0; the empty asm keeps an FMA producing b from fusing with the
       // convert.
-      uint32_t v = (b[k] & 0x7FFFFFFFu) > 0x7F800000u ? 0x7FC00000u : b[k];
+      const float value = __builtin_bit_cast(float, b[k]);
+      uint32_t v = value != value ? 0x7FC00000u : b[k];
       __asm__("" : "+v"(v));
       x[k] = __builtin_bit_cast(float, v);
     }
