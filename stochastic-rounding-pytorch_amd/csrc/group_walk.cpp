@@ -40,6 +40,7 @@
 
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
+#include <structmember.h>
 #include <torch/csrc/autograd/python_variable.h>
 
 #include <algorithm>
@@ -54,6 +55,17 @@ PyObject* g_grad = nullptr;   // interned "grad"
 PyObject* g_step = nullptr;   // interned "step"
 PyObject* g_local = nullptr;  // interned "_local_tensor"
 PyObject* g_spec = nullptr;   // interned "_spec"
+PyObject* g_hash = nullptr;   // interned "__hash__"
+PyObject* g_mesh = nullptr;         // interned DTensorSpec field names
+PyObject* g_placements = nullptr;
+PyObject* g_shard_order = nullptr;
+PyObject* g_tensor_meta = nullptr;
+PyObject* g_tensor_hash = nullptr;  // torch.Tensor.__hash__ (returns id(self))
+PyObject* g_spec_type = nullptr;    // DTensorSpec, once enable_spec_fast_path() vouched for its fields
+// The exact DTensor type and the offsets of its `_local_tensor` and `_spec`
+// slots, once enable_dtensor_slots() found them as object members.
+PyTypeObject* g_dtensor_type = nullptr;
+Py_ssize_t g_local_offset = -1, g_spec_offset = -1;
 
 // Everything one walk collects.
 struct Walk {
@@ -77,7 +89,68 @@ bool describe(PyObject* obj, Walk& w, bool gradient, PyObject* parameter_spec = 
 // A DTensor: a tensor subclass whose data is the `_local_tensor` it carries,
 // laid out by its `_spec` (mesh, placements, global shape).
 bool is_distributed(PyObject* obj) {
+  if (Py_TYPE(obj) == g_dtensor_type) return true;
   return !THPVariable_CheckExact(obj) && PyObject_HasAttr(obj, g_local);
+}
+
+// New reference to a DTensor's `_local_tensor` or `_spec`, or nullptr (no
+// error set).  The exact DTensor type's slots are read at their offsets.
+PyObject* dtensor_part(PyObject* obj, PyObject* name, Py_ssize_t offset) {
+  if (Py_TYPE(obj) == g_dtensor_type && offset >= 0) {
+    PyObject* value = *reinterpret_cast<PyObject**>(reinterpret_cast<char*>(obj) + offset);
+    Py_XINCREF(value);
+    return value;
+  }
+  PyObject* value = PyObject_GetAttr(obj, name);
+  if (value == nullptr) PyErr_Clear();
+  return value;
+}
+
+// One attribute of a spec as a new reference, or nullptr (error cleared).
+PyObject* field(PyObject* spec, PyObject* name) {
+  PyObject* value = PyObject_GetAttr(spec, name);
+  if (value == nullptr) PyErr_Clear();
+  return value;
+}
+
+// Equal by PyObject_RichCompareBool, with no error left set.
+bool same(PyObject* a, PyObject* b) {
+  const int r = PyObject_RichCompareBool(a, b, Py_EQ);
+  if (r < 0) PyErr_Clear();
+  return r == 1;
+}
+
+// True only when DTensorSpec._check_equals(a, b) is certainly true, decided
+// with C-level comparisons: the same mesh object; placements and shard order
+// equal as tuples (their elements compare in C++); tensor metadata both
+// absent, or the same shape, stride and dtype.  False means "undecided".
+bool specs_certainly_equal(PyObject* a, PyObject* b) {
+  if (g_spec_type == nullptr || Py_TYPE(a) != reinterpret_cast<PyTypeObject*>(g_spec_type) ||
+      Py_TYPE(b) != Py_TYPE(a)) {
+    return false;
+  }
+  Ref mesh_a(field(a, g_mesh)), mesh_b(field(b, g_mesh));
+  if (mesh_a.obj == nullptr || mesh_a.obj != mesh_b.obj) return false;
+  for (PyObject* name : {g_placements, g_shard_order}) {
+    Ref x(field(a, name)), y(field(b, name));
+    if (x.obj == nullptr || y.obj == nullptr) return false;
+    if (x.obj != y.obj && !(PyTuple_CheckExact(x.obj) && PyTuple_CheckExact(y.obj) && same(x.obj, y.obj))) {
+      return false;
+    }
+  }
+  Ref meta_a(field(a, g_tensor_meta)), meta_b(field(b, g_tensor_meta));
+  if (meta_a.obj == nullptr || meta_b.obj == nullptr) return false;
+  if (meta_a.obj == Py_None || meta_b.obj == Py_None) return meta_a.obj == meta_b.obj;
+  if (!PyTuple_Check(meta_a.obj) || !PyTuple_Check(meta_b.obj) || PyTuple_GET_SIZE(meta_a.obj) != 3 ||
+      PyTuple_GET_SIZE(meta_b.obj) != 3) {
+    return false;
+  }
+  for (Py_ssize_t k = 0; k < 3; ++k) {  // shape, stride, dtype
+    PyObject* x = PyTuple_GET_ITEM(meta_a.obj, k);
+    PyObject* y = PyTuple_GET_ITEM(meta_b.obj, k);
+    if (x != y && !(PyTuple_Check(x) && PyTuple_Check(y) && same(x, y))) return false;
+  }
+  return true;
 }
 
 // A DTensor parameter's or state's words: its Python type, the identity of
@@ -89,14 +162,15 @@ bool is_distributed(PyObject* obj) {
 // spec must be the parameter's or equal to it, checked here, and only its
 // type and local shard enter the words.
 bool describe_distributed(PyObject* obj, Walk& w, bool gradient, PyObject* parameter_spec) {
-  Ref local(PyObject_GetAttr(obj, g_local));
+  Ref local(dtensor_part(obj, g_local, g_local_offset));
   if (local.obj == nullptr || !THPVariable_Check(local.obj)) return false;
-  Ref spec(PyObject_GetAttr(obj, g_spec));
+  Ref spec(dtensor_part(obj, g_spec, g_spec_offset));
   if (spec.obj == nullptr) return false;
   w.words.push_back(static_cast<int64_t>(reinterpret_cast<intptr_t>(Py_TYPE(obj))));
   if (gradient) {
     if (parameter_spec == nullptr) return false;
-    if (spec.obj != parameter_spec && PyObject_RichCompareBool(spec.obj, parameter_spec, Py_EQ) != 1) {
+    if (spec.obj != parameter_spec && !specs_certainly_equal(spec.obj, parameter_spec) &&
+        PyObject_RichCompareBool(spec.obj, parameter_spec, Py_EQ) != 1) {
       return false;
     }
   } else {
@@ -145,10 +219,33 @@ bool describe(PyObject* obj, Walk& w, bool gradient, PyObject* parameter_spec) {
   }
 }
 
+// True when objects of `type` hash as torch.Tensor does, by id(self).  The
+// last type seen is kept (with a reference, so its address cannot be reused).
+bool hashes_by_id(PyTypeObject* type) {
+  static PyTypeObject* last = nullptr;
+  static bool last_result = false;
+  if (type == last) return last_result;
+  PyObject* method = _PyType_Lookup(type, g_hash);  // borrowed; sets no error
+  Py_INCREF(type);
+  Py_XDECREF(reinterpret_cast<PyObject*>(last));
+  last = type;
+  last_result = method != nullptr && method == g_tensor_hash;
+  return last_result;
+}
+
 // Borrowed state dict of a parameter, or nullptr (without an exception set)
-// when it is absent or not an exact dict.
+// when it is absent or not an exact dict.  A parameter whose type keeps
+// torch.Tensor's id-based hash is looked up with that hash computed here,
+// hash(id(parameter)), instead of calling the Python method.
 PyObject* parameter_state(PyObject* state, PyObject* parameter) {
-  PyObject* entry = PyDict_GetItemWithError(state, parameter);
+  PyObject* entry = nullptr;
+  if (g_tensor_hash != nullptr && hashes_by_id(Py_TYPE(parameter))) {
+    Ref id(PyLong_FromVoidPtr(parameter));
+    const Py_hash_t hash = id.obj == nullptr ? -1 : PyObject_Hash(id.obj);
+    entry = hash == -1 ? nullptr : _PyDict_GetItem_KnownHash(state, parameter, hash);
+  } else {
+    entry = PyDict_GetItemWithError(state, parameter);
+  }
   if (entry == nullptr || !PyDict_CheckExact(entry)) {
     PyErr_Clear();
     return nullptr;
@@ -165,7 +262,7 @@ bool walk_parameter(PyObject* parameter, PyObject* gradient, PyObject* state, Py
   Py_INCREF(entry);
   if (PyList_Append(entries, entry) != 0) return false;
   w.words.push_back(2 + PyTuple_GET_SIZE(names));
-  Ref parameter_spec(is_distributed(parameter) ? PyObject_GetAttr(parameter, g_spec) : nullptr);
+  Ref parameter_spec(is_distributed(parameter) ? dtensor_part(parameter, g_spec, g_spec_offset) : nullptr);
   if (!describe(parameter, w, false) || !describe(gradient, w, true, parameter_spec.obj)) return false;
   for (Py_ssize_t k = 0; k < PyTuple_GET_SIZE(names); ++k) {
     PyObject* tensor = PyDict_GetItemWithError(entry, PyTuple_GET_ITEM(names, k));
@@ -301,7 +398,47 @@ PyObject* set_steps(PyObject*, PyObject* args) {
   Py_RETURN_NONE;
 }
 
+// enable_spec_fast_path(spec_type): compare DTensor gradient specs of this
+// exact type with specs_certainly_equal before falling back to __eq__.  The
+// caller vouches that the type's equality is its mesh, placements, shard
+// order and tensor metadata (shape, stride, dtype).
+PyObject* enable_spec_fast_path(PyObject*, PyObject* args) {
+  PyObject* type;
+  if (!PyArg_ParseTuple(args, "O!", &PyType_Type, &type)) return nullptr;
+  Py_INCREF(type);
+  Py_XSETREF(g_spec_type, type);
+  Py_RETURN_NONE;
+}
+
+// enable_dtensor_slots(dtensor_type): read `_local_tensor` and `_spec` of
+// objects of exactly this type at their slot offsets.  Returns whether both
+// are object members of the type (otherwise attribute lookups stay).
+PyObject* enable_dtensor_slots(PyObject*, PyObject* args) {
+  PyObject* type;
+  if (!PyArg_ParseTuple(args, "O!", &PyType_Type, &type)) return nullptr;
+  Py_ssize_t offsets[2] = {-1, -1};
+  PyObject* names[2] = {g_local, g_spec};
+  for (int k = 0; k < 2; ++k) {
+    PyObject* descr = PyDict_GetItemWithError(reinterpret_cast<PyTypeObject*>(type)->tp_dict, names[k]);
+    if (descr == nullptr || Py_TYPE(descr) != &PyMemberDescr_Type) {
+      PyErr_Clear();
+      Py_RETURN_FALSE;
+    }
+    const PyMemberDef* member = reinterpret_cast<PyMemberDescrObject*>(descr)->d_member;
+    if (member->type != T_OBJECT_EX) Py_RETURN_FALSE;
+    offsets[k] = member->offset;
+  }
+  Py_INCREF(type);
+  Py_XDECREF(reinterpret_cast<PyObject*>(g_dtensor_type));
+  g_dtensor_type = reinterpret_cast<PyTypeObject*>(type);
+  g_local_offset = offsets[0];
+  g_spec_offset = offsets[1];
+  Py_RETURN_TRUE;
+}
+
 PyMethodDef kMethods[] = {
+    {"enable_dtensor_slots", enable_dtensor_slots, METH_VARARGS, "enable_dtensor_slots(dtensor_type) -> bool"},
+    {"enable_spec_fast_path", enable_spec_fast_path, METH_VARARGS, "enable_spec_fast_path(spec_type)"},
     {"group_signature", group_signature, METH_VARARGS,
      "group_signature(params, state, state_names, uses_step, first_index)"},
     {"spans_disjoint", spans_disjoint, METH_VARARGS, "spans_disjoint(spans) -> bool"},
@@ -319,6 +456,21 @@ PyMODINIT_FUNC PyInit__group_walk() {
   g_step = PyUnicode_InternFromString("step");
   g_local = PyUnicode_InternFromString("_local_tensor");
   g_spec = PyUnicode_InternFromString("_spec");
-  if (g_grad == nullptr || g_step == nullptr || g_local == nullptr || g_spec == nullptr) return nullptr;
+  g_hash = PyUnicode_InternFromString("__hash__");
+  g_mesh = PyUnicode_InternFromString("mesh");
+  g_placements = PyUnicode_InternFromString("placements");
+  g_shard_order = PyUnicode_InternFromString("shard_order");
+  g_tensor_meta = PyUnicode_InternFromString("tensor_meta");
+  for (PyObject* name : {g_grad, g_step, g_local, g_spec, g_hash, g_mesh, g_placements, g_shard_order, g_tensor_meta}) {
+    if (name == nullptr) return nullptr;
+  }
+  // torch.Tensor.__hash__, for the id-hash lookups; without it every
+  // lookup calls the type's __hash__.
+  PyObject* torch = PyImport_ImportModule("torch");
+  PyObject* tensor = torch ? PyObject_GetAttrString(torch, "Tensor") : nullptr;
+  g_tensor_hash = tensor ? PyObject_GetAttr(tensor, g_hash) : nullptr;
+  Py_XDECREF(tensor);
+  Py_XDECREF(torch);
+  PyErr_Clear();
   return PyModule_Create(&kModule);
 }

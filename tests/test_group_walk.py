@@ -12,6 +12,7 @@ validating path would.  The kernel launch is replaced by a recorder.
 from __future__ import annotations
 
 import copy
+import sys
 import importlib
 from contextlib import nullcontext
 
@@ -443,3 +444,144 @@ def test_dtensor_groups_are_described_by_their_local_shards():
     # A state replaced by another DTensor changes the layout.
     state[params[2]]["exp_avg"] = torch.zeros_like(params[2])
     assert _sig(params, state)[0] != second[0]
+
+
+def _python_calls(params, state):
+    """Python-level functions called while the native walk describes a group."""
+    calls = []
+    previous = sys.getprofile()
+    sys.setprofile(lambda frame, event, arg: calls.append(frame.f_code.co_name) if event == "call" else None)
+    try:
+        _group_walk.group_signature(params, state, NAMES, True, 0)
+    finally:
+        sys.setprofile(previous)
+    return calls
+
+
+_MESHES = iter(range(1 << 30))
+
+
+def _fresh_dtensor_group(n):
+    """_dtensor_group on a mesh no earlier test built.
+
+    DTensor caches sharding results by mesh equality, so from_local on a mesh
+    equal to an earlier one can return specs holding that earlier mesh object.
+    """
+    from test_dtensor import _dtensor
+    from torch.distributed.device_mesh import DeviceMesh
+    from torch.distributed.tensor import Shard
+
+    mesh = DeviceMesh("cpu", torch.arange(2), mesh_dim_names=(f"walk{next(_MESHES)}",), _init_backend=False, _rank=1)
+    params = [torch.nn.Parameter(_dtensor(torch.randn(7, 3), mesh, (Shard(0),))) for _ in range(n)]
+    for p in params:
+        p.grad = _dtensor(torch.randn(7, 3), mesh, (Shard(0),))
+    state = {p: {"exp_avg": torch.zeros_like(p), "exp_avg_sq": torch.zeros_like(p)} for p in params}
+    return mesh, params, state
+
+
+def _gradient_with_spec(parameter, spec):
+    from torch.distributed.tensor import DTensor
+
+    return DTensor(torch.randn_like(parameter._local_tensor), spec, requires_grad=False)
+
+
+def test_steady_signatures_make_no_python_calls():
+    """State lookups hash parameters by id natively, and DTensor gradient specs compare in C.
+
+    FSDP2 builds each gradient with its parameter's own spec object
+    (_fsdp_param.py, to_sharded_dtensor); DTensor.from_local builds an equal
+    new one.  Neither, nor a plain group, runs Python code in the walk.
+    """
+    from test_dtensor import _dtensor
+
+    from sr_states import _group_walk
+    from torch.distributed.tensor import DTensor, Shard
+
+    assert _group_walk.enable_dtensor_slots(DTensor)
+    mesh, params, state = _fresh_dtensor_group(n=4)
+    plain = [torch.nn.Parameter(torch.randn(5, 3)) for _ in range(4)]
+    for p in plain:
+        p.grad = torch.randn(5, 3)
+    plain_state = {p: {"exp_avg": torch.zeros_like(p), "exp_avg_sq": torch.zeros_like(p)} for p in plain}
+    assert _sig(plain, plain_state) is not None and _python_calls(plain, plain_state) == []
+    for p in params:
+        p.grad = _gradient_with_spec(p, p._spec)
+    assert _sig(params, state) is not None and _python_calls(params, state) == []
+    for p in params:
+        p.grad = _dtensor(torch.randn(7, 3), mesh, (Shard(0),))
+        assert p.grad._spec is not p._spec and p.grad._spec.mesh is p._spec.mesh
+    assert _sig(params, state) is not None and _python_calls(params, state) == []
+
+
+def test_native_spec_comparison_agrees_with_dtensorspec_equality():
+    """A gradient is vouched for exactly when its spec equals its parameter's (DTensorSpec.__eq__)."""
+    import copy
+
+    from test_dtensor import _mesh
+
+    from torch.distributed.tensor import Replicate, Shard
+    from torch.distributed.tensor._dtensor_spec import DTensorSpec, TensorMeta
+
+    mesh, params, state = _fresh_dtensor_group(n=1)
+    (p,) = params
+    spec = p._spec
+    meta = spec.tensor_meta
+    variants = {
+        "equal, new objects": DTensorSpec(mesh, (Shard(0),), TensorMeta(torch.Size(meta.shape), tuple(meta.stride), meta.dtype)),
+        "equal, copied mesh": DTensorSpec(copy.copy(mesh), spec.placements, meta),
+        "mesh with other dimension names": DTensorSpec(_mesh((2,), 1), spec.placements, meta),
+        "other placement": DTensorSpec(mesh, (Shard(1),), meta),
+        "replicated": DTensorSpec(mesh, (Replicate(),), meta),
+        "other shape": DTensorSpec(mesh, spec.placements, TensorMeta(torch.Size((6, 3)), meta.stride, meta.dtype)),
+        "other stride": DTensorSpec(mesh, spec.placements, TensorMeta(meta.shape, (1, 7), meta.dtype)),
+        "other dtype": DTensorSpec(mesh, spec.placements, TensorMeta(meta.shape, meta.stride, torch.float64)),
+        "no metadata": DTensorSpec(mesh, spec.placements, None),
+        "other mesh": DTensorSpec(_mesh((2,), 0), spec.placements, meta),
+    }
+    outcomes = []
+    for name, other in variants.items():
+        try:
+            p.grad = _gradient_with_spec(p, other)
+        except RuntimeError:  # autograd refuses gradients of another size or dtype
+            continue
+        vouched = _sig(params, state) is not None
+        assert vouched == (other == spec), name
+        outcomes.append((name, vouched))
+    assert sum(v for _, v in outcomes) >= 2 and sum(not v for _, v in outcomes) >= 4, outcomes
+
+
+def test_dtensor_signatures_of_148_parameters_take_well_under_a_millisecond():
+    """Steady-state host cost of a 148-parameter DTensor group (min of many runs, loose bound).
+
+    Measured here at 0.09-0.17 ms (FSDP2-style gradients) and 0.2-0.25 ms
+    (from_local gradients), against 0.04-0.07 ms for 148 plain parameters;
+    the validating walk takes about 15 ms.  That no Python code runs in the
+    walk is pinned exactly by test_steady_signatures_make_no_python_calls.
+    """
+    import time
+
+    from test_dtensor import _dtensor
+
+    from torch.distributed.tensor import Shard
+
+    mesh, params, state = _fresh_dtensor_group(n=148)
+
+    def best(regrad):
+        fastest = float("inf")
+        for _ in range(40):
+            regrad()
+            start = time.perf_counter()
+            assert _sig(params, state) is not None
+            fastest = min(fastest, time.perf_counter() - start)
+        return fastest
+
+    def fsdp2_grads():
+        for q in params:
+            q.grad = _gradient_with_spec(q, q._spec)
+
+    def from_local_grads():
+        for q in params:
+            q.grad = _dtensor(torch.randn(7, 3), mesh, (Shard(0),))
+
+    assert best(fsdp2_grads) < 1e-3
+    assert best(from_local_grads) < 1e-3
