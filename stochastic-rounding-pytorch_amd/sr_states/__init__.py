@@ -1,8 +1,10 @@
 """SR-States for MI355X: stochastic-rounding optimizer states on gfx950.
 
 The public surface follows the reference package ``sr_states``:
-``StateFormat``, ``StateOptimizer``, ``cast`` and ``register_rounding`` at
-the top level, and the fused optimizers and casts in ``sr_states.hip`` (the
+``StateFormat``, ``StateOptimizer``, ``cast``, ``register_rounding`` and the
+per-parameter optimizers ``AdamWReferenceSR/RN`` and ``SGDMReferenceSR/RN``
+at the top level, the functional updates in ``sr_states.reference``, and the
+fused multi-tensor optimizers and casts in ``sr_states.hip`` (the
 counterpart of ``sr_states.triton``).  All arithmetic runs in the HIP
 library ``libsr_states_hip.so``; there is no CPU execution path.
 """
@@ -21,13 +23,18 @@ from .hip import (
     sr_cast_bf16,
 )
 from .optim._state import StateOptimizer
+from .optim.eager import AdamWReferenceRN, AdamWReferenceSR, SGDMReferenceRN, SGDMReferenceSR
 from .rounding import cast, register_rounding
 
 __all__ = [
     "AdamWHip",
     "AdamWHipRN",
+    "AdamWReferenceRN",
+    "AdamWReferenceSR",
     "SGDMHip",
     "SGDMHipRN",
+    "SGDMReferenceRN",
+    "SGDMReferenceSR",
     "StateFormat",
     "StateOptimizer",
     "cast",

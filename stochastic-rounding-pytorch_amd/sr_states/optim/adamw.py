@@ -37,3 +37,12 @@ def adamw_hparams(lr, beta1, beta2, eps, weight_decay, step) -> _lib.AdamWHparam
         decay=1.0 - lr * weight_decay,
         eps=eps,
     )
+
+
+def __getattr__(name):
+    """``AdamWReferenceSR``/``AdamWReferenceRN``, defined with the other per-parameter optimizers."""
+    if name in ("AdamWReferenceSR", "AdamWReferenceRN"):
+        from . import eager
+
+        return getattr(eager, name)
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")

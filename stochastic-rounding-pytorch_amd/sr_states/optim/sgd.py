@@ -18,3 +18,12 @@ def validate_sgdm(group):
 def sgdm_hparams(lr, momentum) -> _lib.SgdmHparams:
     """FP32 scalars of ``u = u*momentum + g; p = p + (-lr)*u`` (reference/sgd.py:62-64)."""
     return _lib.SgdmHparams(momentum=momentum, neg_lr=-lr)
+
+
+def __getattr__(name):
+    """``SGDMReferenceSR``/``SGDMReferenceRN``, defined with the other per-parameter optimizers."""
+    if name in ("SGDMReferenceSR", "SGDMReferenceRN"):
+        from . import eager
+
+        return getattr(eager, name)
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")

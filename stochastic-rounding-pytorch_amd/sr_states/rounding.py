@@ -68,6 +68,12 @@ def validate_rounding(dtype: torch.dtype, rounding: str, *, backend: str = "refe
         raise ValueError(f"rounding {rounding!r} for {dtype} has no HIP implementation")
 
 
+def has_native(dtype: torch.dtype, rounding: str) -> bool:
+    """Whether a registered (dtype, rule) pair runs inside the fused HIP kernels."""
+    routine = _ROUTINES.get((dtype, rounding))
+    return routine is not None and routine.native is not None
+
+
 def native_codes(dtype: torch.dtype, rounding: str) -> tuple[int, int]:
     """(sr_dtype, sr_rule) of a rule with a HIP implementation."""
     validate_rounding(dtype, rounding, backend="hip")
