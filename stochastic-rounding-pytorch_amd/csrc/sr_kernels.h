@@ -177,7 +177,11 @@ __device__ __forceinline__ void load_lane_group(const char* tile, uint32_t j, ui
 
 template <int ENC>
 __device__ __forceinline__ void store_lane_group(char* tile, uint32_t j, const uint32_t (&words)[group_words(ENC)]) {
-  store_words<kGroup * enc_bytes(ENC)>(tile + j * static_cast<uint32_t>(kGroup * enc_bytes(ENC)), words);
+  // The offset is recomputed behind an empty asm: sharing it with the load
+  // of the same tile made the compiler form full 64-bit store addresses.
+  uint32_t offset = j * static_cast<uint32_t>(kGroup * enc_bytes(ENC));
+  __asm__("" : "+v"(offset));
+  store_words<kGroup * enc_bytes(ENC)>(tile + offset, words);
 }
 
 template <int ENC>
@@ -255,8 +259,27 @@ __device__ __forceinline__ void adamw_vector(char* p, const char* g, char* m, ch
       if (sqrt_needs_library(vo[k])) root[k] = sqrt_library(vo[k]);
     }
   }
+  // numer / den through div_short where its domain holds: eps, uniform, in
+  // its range and every |q0| in range (an infinite or NaN denominator fails
+  // the latter).  Otherwise the lane computes its E denominators and
+  // quotients again, exactly, with the library division (one branch, which
+  // whole waves skip).
+  float numer[E], den[E], quotient[E];
+  bool divide_again = !short_division_eps(s.eps);
 #pragma unroll
-  for (int k = 0; k < E; ++k) pf[k] = adamw_parameter(pf[k], mo[k], root[k], s);
+  for (int k = 0; k < E; ++k) {
+    numer[k] = s.neg_step_size * mo[k];
+    den[k] = adamw_denominator_finite(root[k], s);
+    bool ok;
+    quotient[k] = div_short(numer[k], den[k], ok);
+    divide_again |= !ok;
+  }
+  if (divide_again) {
+#pragma unroll
+    for (int k = 0; k < E; ++k) quotient[k] = div_library(numer[k], adamw_denominator(root[k], s));
+  }
+#pragma unroll
+  for (int k = 0; k < E; ++k) pf[k] = pf[k] * s.decay + quotient[k];
   encode_group<PE>(pf, 0u, wp);
   encode_group<ME>(mo, cm + index, wm);
   encode_group<VE>(vo, cv + index, wv);

@@ -504,6 +504,41 @@ SR_HD uint32_t minifloat_grid_bits(uint32_t b, uint32_t hash, uint32_t subnormal
   }
 }
 
+// The stochastic grid value of minifloat_grid_bits<F, true> for the FP8
+// formats (M <= 3) in one computation, with no branch between the normal
+// and the subnormal range.  |b|, clamped to the largest finite value, is
+// scaled by the power of two that makes the grid spacing there -- 2^(e-M) in
+// the binade of 2^e, 2^(emin-M) below 2^emin -- equal to 2^24.  The product
+// is exact and below 2^(25+M) <= 2^28, so its truncated integer y holds the
+// grid index above bit 24 and, below it, the integer form's 24-bit threshold
+// T (the dropped fraction times 2^24, truncated).  (y + (~hash >> 8)) >> 24
+// is then the index plus one iff (hash >> 8) < T, and the rounded value is
+// that index times the spacing (exact: the index is at most 2^(M+1)).  For
+// every b that is not a NaN (NaN gives an unspecified value).  `low24` and
+// `magnitude` are the constants 0x00FFFFFF and 0x7FFFFFFF; a caller encoding
+// several elements passes them in scalar registers, where the three-operand
+// instructions that fold the xor into the add and the sign merge take them
+// (these instructions take no literal operand).
+template <class F>
+SR_HD uint32_t fp8_sr_grid_bits(uint32_t b, uint32_t hash, uint32_t low24 = 0x00FFFFFFu,
+                                uint32_t magnitude = 0x7FFFFFFFu) {
+  static_assert(F::kWidth == 8 && F::kSat && F::kM <= 3, "FP8 formats only");
+  // Scale exponent 151 + M - e in the binade of 2^e (from the exponent field),
+  // at most 151 - emin + M; spacing exponent 24 less than minus the scale's.
+  constexpr uint32_t kScaleOfExponent = (278u + F::kM) << 23;
+  constexpr uint32_t kScaleBelowNormal = static_cast<uint32_t>(151 - F::kEmin + F::kM) << 23;
+  constexpr uint32_t kSpacingOfScale = 278u << 23;
+  // |b| clamped to the largest finite value (+-Inf to it as well).
+  const float clamped = fminf(fabsf(bits_f32(b)), bits_f32(F::kMaxBits));
+  const uint32_t from_exponent = kScaleOfExponent - (f32_bits(clamped) & 0x7F800000u);
+  const uint32_t scale = from_exponent < kScaleBelowNormal ? from_exponent : kScaleBelowNormal;
+  const uint32_t y = static_cast<uint32_t>(clamped * bits_f32(scale));
+  // ~hash >> 8 is the 24-bit complement of hash >> 8.
+  const uint32_t index = (((hash >> 8) ^ low24) + y) >> 24;
+  const float value = static_cast<float>(index) * bits_f32(kSpacingOfScale - scale);
+  return b ^ ((b ^ f32_bits(value)) & magnitude);  // value's magnitude, b's sign
+}
+
 // Decodes one group of storage words of ENC.
 template <int ENC>
 SR_HD void decode_group(const uint32_t (&words)[group_words(ENC)], float (&x)[kGroup]) {
@@ -550,21 +585,32 @@ SR_HD void encode_group_with(const uint32_t (&b)[kGroup], const uint32_t (&hash)
     }
   } else if constexpr (ENC == ENC_BF16_RN) {
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    // The sum of the group is NaN if any element is (or for opposite
+    // infinities): then every element takes the integer form bf16_rn_bits,
+    // whose NaN is the reference's 0x7FC0 whatever the payload (rare; whole
+    // waves skip it; a convert there would be shared with the pairs below
+    // and split them).
+    uint32_t bits[kGroup];
     float x[kGroup];
 #pragma unroll
     for (int k = 0; k < kGroup; ++k) {
-      // NaN becomes the quiet NaN whose nearest BF16 is the reference's
-      // 0x7FC0; the empty asm keeps an FMA producing b from fusing with the
-      // convert.
-      const float value = __builtin_bit_cast(float, b[k]);
-      uint32_t v = value != value ? 0x7FC00000u : b[k];
-      __asm__("" : "+v"(v));
-      x[k] = __builtin_bit_cast(float, v);
+      // The empty asm keeps an FMA producing b from fusing with the convert.
+      bits[k] = b[k];
+      __asm__("" : "+v"(bits[k]));
+      x[k] = __builtin_bit_cast(float, bits[k]);
     }
+    const float sum = (x[0] + x[1]) + (x[2] + x[3]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const bf16x2 pair = {static_cast<__bf16>(x[2 * j]), static_cast<__bf16>(x[2 * j + 1])};
       words[j] = __builtin_bit_cast(uint32_t, pair);
+    }
+    if (sum != sum) {
+      __asm__ volatile("");
+      uint32_t codes[kGroup];
+#pragma unroll
+      for (int k = 0; k < kGroup; ++k) codes[k] = bf16_rn_bits(bits[k]);
+      pack_group<ENC>(codes, words);
     }
   } else {
     using F = typename std::conditional<ENC == ENC_F16_RN || ENC == ENC_F16_SR, F16,
@@ -572,12 +618,17 @@ SR_HD void encode_group_with(const uint32_t (&b)[kGroup], const uint32_t (&hash)
     constexpr bool kStoch = enc_stochastic(ENC);
     uint32_t grid[kGroup];
     bool nan = false;
-    uint32_t subnormal = kSubnormalBits<F>;
-    __asm__("" : "+v"(subnormal));  // one register for the group's four selects
+    uint32_t subnormal = kSubnormalBits<F>, low24 = 0x00FFFFFFu, magnitude = 0x7FFFFFFFu;
+    if constexpr (kStoch && F::kWidth == 8) {
+      __asm__("" : "+s"(low24), "+s"(magnitude));  // one scalar register each
+    } else {
+      __asm__("" : "+v"(subnormal));  // one register for the group's four selects
+    }
 #pragma unroll
     for (int k = 0; k < kGroup; ++k) {
-      nan |= (b[k] & 0x7FFFFFFFu) > 0x7F800000u;
-      grid[k] = minifloat_grid_bits<F, kStoch>(b[k], hash[k], subnormal);
+      nan |= bits_f32(b[k]) != bits_f32(b[k]);
+      if constexpr (kStoch && F::kWidth == 8) grid[k] = fp8_sr_grid_bits<F>(b[k], hash[k], low24, magnitude);
+      else grid[k] = minifloat_grid_bits<F, kStoch>(b[k], hash[k], subnormal);
       __asm__("" : "+v"(grid[k]));  // no fusing of an FMA into the convert
     }
     float g[kGroup];
@@ -652,20 +703,21 @@ struct AdamWScalars {
 constexpr float kMinCorrection2Sqrt = 0x1p-27f;
 
 // IEEE square root, correctly rounded, for |v| >= 2^-96, zero, infinite
-// and NaN v.  On the device: the hardware estimate, which is within one
-// ulp, corrected to the nearest by the signs of v - s*(s - ulp) and
-// v - s*(s + ulp) (s*(s -/+ ulp) is the square of the midpoint below/above
-// s, less ulp^2/4, and no float lies strictly between the two).  Below
-// 2^-96 the residuals can lose their sign: sqrt_needs_library() marks those
-// inputs, for which the caller takes sqrtf.  Checked, with that fallback,
-// against sqrtf on every FP32 input.
+// and NaN v.  On the device: y = the hardware 1/sqrt(v) estimate,
+// s0 = RN(v y), and one Newton step with the exact residual,
+// RN(s0 + RN(v - s0^2) * RN(y / 2)).  A device check found this equal to
+// the correctly rounded root for every v in [2^-96, +Inf); zero and +Inf,
+// where s0 is 0 * Inf, return v itself, and negative v and NaN give NaN
+// through y.  Below 2^-96 the residual loses bits: sqrt_needs_library()
+// marks those inputs, for which the caller takes sqrtf.  Checked, with that
+// fallback, against sqrtf on every FP32 input.
 SR_HD float sqrt_rn_wide(float v) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  const float s = __builtin_amdgcn_sqrtf(v);
-  const float below = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, s) - 1u);
-  const float above = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, s) + 1u);
-  const float down = fmaf(-below, s, v) <= 0.0f ? below : s;
-  return fmaf(-above, s, v) > 0.0f ? above : down;
+  const float y = __builtin_amdgcn_rsqf(v);
+  const float s0 = v * y;
+  const float root = fmaf(fmaf(-s0, s0, v), 0.5f * y, s0);
+  constexpr int kZeroOrInf = 32 | 64 | 512;  // -0, +0, +Inf
+  return __builtin_amdgcn_classf(v, kZeroOrInf) ? v : root;
 #else
   return sqrtf(v);
 #endif
@@ -733,12 +785,79 @@ SR_HD void adamw_moments(float g, float m, float v, const AdamWScalars& s, float
   v_out = fmaf(g_scaled, g, v_scaled);
 }
 
+// The denominator sqrt(v') / sqrt(1-beta2^t) + eps from root = sqrt(v').
+SR_HD float adamw_denominator(float root, const AdamWScalars& s) {
+  return div_by_constant(root, s.correction2_sqrt, s.inv_correction2_sqrt) + s.eps;
+}
+
+// The same without div_by_constant's selection of q0: equal to it for every
+// finite root when eps > 0 (the selection matters for an infinite root, and
+// for the sign of a zero root, which adding a positive eps removes).  The
+// vector path's division falls back, recomputing adamw_denominator, wherever
+// the result is infinite or NaN.
+SR_HD float adamw_denominator_finite(float root, const AdamWScalars& s) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float q0 = root * s.inv_correction2_sqrt;
+  return fmaf(fmaf(-q0, s.correction2_sqrt, root), s.inv_correction2_sqrt, q0) + s.eps;
+#else
+  return adamw_denominator(root, s);
+#endif
+}
+
 // The parameter from the unrounded m' and root = sqrt(v').
 SR_HD float adamw_parameter(float p, float m_out, float root, const AdamWScalars& s) {
-  const float den = div_by_constant(root, s.correction2_sqrt, s.inv_correction2_sqrt) + s.eps;
   const float numer = s.neg_step_size * m_out;
   const float p_decayed = p * s.decay;
-  return p_decayed + numer / den;
+  return p_decayed + numer / adamw_denominator(root, s);
+}
+
+// Domain of div_short for the AdamW denominator: with eps in [2^-60, 2^100]
+// every finite denominator sqrt(v') / c + eps lies in [2^-60, 2^101), since
+// sqrt(v') < 2^64 and c >= 2^-27.  A launch-uniform test on eps's bits.
+SR_HD bool short_division_eps(float eps) {
+  const uint32_t e = f32_bits(eps);
+  return e >= 0x21800000u && e <= 0x71800000u;  // 2^-60 .. 2^100
+}
+
+// RN(1/b) for every b in [2^-126, 2^126): the hardware reciprocal estimate
+// y0 and one Newton step, RN(y0 + RN(1 - b y0) y0).  A device check compares
+// it with 1.0f / b on every float of that range.
+SR_HD float rcp_rn(float b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float y0 = __builtin_amdgcn_rcpf(b);
+  return fmaf(fmaf(-b, y0, 1.0f), y0, y0);
+#else
+  return 1.0f / b;
+#endif
+}
+
+// a / b, correctly rounded, wherever `ok` comes back true, for b in
+// [2^-60, 2^101).  On the device: y = rcp_rn(b) = RN(1/b), q0 = RN(a y),
+// and Markstein's correction by the exact remainder a - b q0.  `ok` is false unless |q0| lies in [2^-40, 2^100): there q0,
+// the quotient and the remainder stay clear of underflow and overflow
+// (|a| >= 2^-101), so scaling a or b by a power of two scales every
+// intermediate exactly, and a device check of every pair of significands
+// covers the whole domain.  Zero, infinite and NaN quotients come back with
+// ok false.  The caller divides again with the library where ok is false.
+SR_HD float div_short(float a, float b, bool& ok) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float y = rcp_rn(b);
+  const float q0 = a * y;
+  ok = __builtin_fabsf(q0) >= 0x1p-40f && __builtin_fabsf(q0) < 0x1p100f;
+  return fmaf(fmaf(-b, q0, a), y, q0);
+#else
+  ok = true;
+  return a / b;
+#endif
+}
+
+// a / b through the library's correctly rounded sequence, behind a side
+// effect the compiler may not hoist (as sqrt_library).
+SR_HD float div_library(float a, float b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __asm__ volatile("" : "+v"(a));
+#endif
+  return a / b;
 }
 
 SR_HD void adamw_update(float p, float g, float m, float v, const AdamWScalars& s,

@@ -1,7 +1,8 @@
-// Exhaustive device check of the AdamW update's square root and division
-// by sqrt(1 - beta2^t): sr::sqrt_rn and sr::div_by_constant against the
-// IEEE correctly rounded sqrtf and x / c (this file is built, like the
-// library, with -fhip-fp32-correctly-rounded-divide-sqrt).
+// Exhaustive device check of the AdamW update's square root and divisions:
+// sr::sqrt_rn, sr::div_by_constant (by sqrt(1 - beta2^t)) and sr::div_short
+// (by the denominator) against the IEEE correctly rounded sqrtf and
+// division (this file is built, like the library, with
+// -fhip-fp32-correctly-rounded-divide-sqrt).
 //   sqrt_rn:         every FP32 input; equal bits, or NaN for NaN.
 //   div_by_constant: every pair of significands, x in [1, 2) and c in
 //                    [1/2, 1), with r = 1 / c correctly rounded; in the
@@ -10,6 +11,14 @@
 //                    two scales every intermediate exactly, so these pairs
 //                    stand for all.  A second kernel runs x = 0, infinity
 //                    and NaN, and both ends of the exponent ranges.
+//   div_short:       every pair of significands (a and b in [1, 2)), where
+//                    the result must be accepted and equal a / b; in its
+//                    domain (b in [2^-60, 2^101), |q0| in [2^-40, 2^100))
+//                    scaling a or b by a power of two scales every
+//                    intermediate exactly, so these pairs stand for all;
+//                    rcp_rn on every float of [2^-126, 2^126); and hashed
+//                    cases over the whole domain, special dividends and
+//                    divisors, and first quotients at both ends of the range.
 // Built by tests/native/build_checks.py into tests/native/libdivsqrt_check.so
 // and run by tests/test_gpu_divsqrt_check.py.
 #include <hip/hip_runtime.h>
@@ -88,6 +97,70 @@ __global__ void edges(unsigned long long* counters) {
   add(counters, mismatches, checks);
 }
 
+// div_short (the AdamW update's division by its denominator) on every pair
+// of significands: thread t takes divisor significand b_first + (t >> 9) and
+// 2^14 dividends, as every_pair.  In [1, 2) x [1, 2) every first quotient is
+// in range, so `ok` must hold; counters[2] counts where it does not.
+__global__ void every_short_pair(uint32_t b_first, unsigned long long* counters) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  const float b = __builtin_bit_cast(float, 0x3F800000u | (b_first + (t >> kXShift)));
+  const uint32_t a_first = (t & ((1u << kXShift) - 1u)) << (23 - kXShift);
+  unsigned long long mismatches = 0, refused = 0;
+  for (uint32_t k = 0; k < (1u << (23 - kXShift)); ++k) {
+    const float a = __builtin_bit_cast(float, 0x3F800000u | (a_first + k));
+    bool ok;
+    const float q = sr::div_short(a, b, ok);
+    mismatches += ok && !same(q, a / b);
+    refused += !ok;
+  }
+  add(counters, mismatches + refused, 1u << (23 - kXShift));
+}
+
+// rcp_rn on every float in [2^-126, 2^126) (2^31 threads from `base`).
+__global__ void every_reciprocal(uint32_t base, unsigned long long* counters) {
+  const uint32_t bits = base + blockIdx.x * blockDim.x + threadIdx.x;
+  const bool in_range = bits >= 0x00800000u && bits < 0x7E800000u;
+  const float b = __builtin_bit_cast(float, bits);
+  add(counters, in_range && !same(sr::rcp_rn(b), 1.0f / b), in_range);
+}
+
+// div_short over its whole domain, 2^9 cases per thread from hashed bits:
+// divisors in [2^-60, 2^101), dividends of every exponent, where `ok` holds
+// the quotient must equal a / b; dividends 0, +-Inf and NaN, and infinite
+// and NaN divisors, must come back with ok false; and first quotients next
+// to both ends of the range, 2^-40 and 2^100.  counters[0] counts wrong
+// quotients with ok and special cases with ok; [1] the cases; [2] those
+// with ok.
+__global__ void short_domain(unsigned long long* counters, unsigned long long* accepted) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  unsigned long long bad = 0, cases = 0, oks = 0;
+  for (uint32_t k = 0; k < 512; ++k) {
+    const uint32_t h1 = sr::h32(t * 512u + k), h2 = sr::h32(h1 ^ 0x85EBCA6Bu), h3 = sr::h32(h2 + 0x68E31DA4u);
+    const uint32_t b_exp = 127u - 60u + (h1 >> 24) % 161u;  // 2^-60 .. 2^100
+    const float b = __builtin_bit_cast(float, (b_exp << 23) | (h2 & 0x7FFFFFu));
+    // Dividends of every exponent, and dividends that put q0 at the ends.
+    float a = __builtin_bit_cast(float, (h3 & 0x80000000u) | (((h1 >> 8) % 255u) << 23) | (h3 & 0x7FFFFFu));
+    if ((k & 3u) == 1u) a = b * (0x1p-40f * (1.0f + (h3 & 0xFFu) * 0x1p-22f - 0x1p-16f));
+    if ((k & 3u) == 2u) a = b * (0x1p100f * (1.0f + (h3 & 0xFFu) * 0x1p-22f - 0x1p-16f));
+    bool ok;
+    const float q = sr::div_short(a, b, ok);
+    bad += ok && !same(q, a / b);
+    oks += ok;
+    ++cases;
+    const float specials[4] = {0.0f, __builtin_inff(), -__builtin_inff(), __builtin_nanf("")};
+    const float sa = (h1 & 1u) ? -specials[k & 3u] : specials[k & 3u];
+    (void)sr::div_short(sa, b, ok);
+    bad += ok;
+    const float sb = (k & 4u) ? __builtin_inff() : __builtin_nanf("");
+    (void)sr::div_short(a, sb, ok);
+    bad += ok;
+    cases += 2;
+  }
+  add(counters, bad, cases);
+  const unsigned long long o = wave_sum(oks);
+  if ((threadIdx.x & 63) == 0) atomicAdd(accepted, o);
+}
+
 hipError_t run(unsigned long long* counters_host, hipError_t (*launches)(unsigned long long*)) {
   unsigned long long* counters = nullptr;
   hipError_t err = hipMalloc(&counters, 2 * sizeof(unsigned long long));
@@ -132,6 +205,47 @@ extern "C" int sr_check_div_by_constant(uint32_t c_first, uint32_t c_count, unsi
     hipLaunchKernelGGL(every_pair, dim3(g_c_count << kXShift >> 8), dim3(256), 0, 0, g_c_first, counters);
     return hipGetLastError();
   }));
+}
+
+// div_short: divisor significands [b_first, b_first + b_count) against every
+// dividend significand (b_count * 2^23 comparisons; mismatches include
+// refusals); ranges as sr_check_div_by_constant.
+extern "C" int sr_check_div_short(uint32_t b_first, uint32_t b_count, unsigned long long* counters_host) {
+  if (b_count == 0 || b_first > (1u << 23) || b_count > (1u << 23) - b_first) return -1;
+  g_c_first = b_first;
+  g_c_count = b_count;
+  return static_cast<int>(run(counters_host, [](unsigned long long* counters) {
+    hipLaunchKernelGGL(every_short_pair, dim3(g_c_count << kXShift >> 8), dim3(256), 0, 0, g_c_first, counters);
+    return hipGetLastError();
+  }));
+}
+
+// rcp_rn on every float in [2^-126, 2^126) (0x7E000000 comparisons).
+extern "C" int sr_check_rcp_rn(unsigned long long* counters_host) {
+  return static_cast<int>(run(counters_host, [](unsigned long long* counters) {
+    hipError_t err = hipSuccess;
+    for (uint32_t half = 0; err == hipSuccess && half < 2; ++half) {
+      hipLaunchKernelGGL(every_reciprocal, dim3(1u << 23), dim3(256), 0, 0, half << 31, counters);
+      err = hipGetLastError();
+    }
+    return err;
+  }));
+}
+
+// div_short over its domain: 2^16 threads x 512 cases x 3 (counters_host[0]
+// bad, [1] cases), and counters_host[2] = the random cases accepted (ok).
+extern "C" int sr_check_div_short_domain(unsigned long long* counters_host) {
+  unsigned long long* counters = nullptr;
+  hipError_t err = hipMalloc(&counters, 3 * sizeof(unsigned long long));
+  if (err == hipSuccess) err = hipMemset(counters, 0, 3 * sizeof(unsigned long long));
+  if (err == hipSuccess) {
+    hipLaunchKernelGGL(short_domain, dim3(256), dim3(256), 0, 0, counters, counters + 2);
+    err = hipGetLastError();
+  }
+  if (err == hipSuccess) err = hipDeviceSynchronize();
+  if (err == hipSuccess) err = hipMemcpy(counters_host, counters, 3 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  if (counters) (void)hipFree(counters);
+  return static_cast<int>(err);
 }
 
 // Zero, infinite and NaN dividends (once per thread) and both ends of the

@@ -41,7 +41,29 @@ unsigned long long sweep(const char* name) {
   return mismatches;
 }
 
+// sr::fp8_sr_grid_bits (the kernels' single-form FP8 stochastic rounding)
+// gives the rounded value; its encoding, by the integer nearest form (the
+// value is exactly representable), must equal the integer stochastic form's.
+template <class F>
+unsigned long long sweep_fp8(const char* name) {
+  unsigned long long mismatches = 0, checks = 0;
+  for (uint64_t x = 0; x < (1ull << 32); x += 257) {
+    const uint32_t b = static_cast<uint32_t>(x);
+    if ((b & 0x7FFFFFFFu) > 0x7F800000u) continue;  // NaN groups take the single-element form
+    const uint32_t th = threshold<F>(b);
+    const uint32_t randoms[6] = {th ? ((th - 1u) << 8) | 0xFFu : 0u, th << 8, (th << 8) | 0xFFu, 0u,
+                                 0xFFFFFFFFu, sr::h32(b ^ 0x5bd1e995u)};
+    for (uint32_t r : randoms) {
+      mismatches += sr::minifloat_bits<F, false>(sr::fp8_sr_grid_bits<F>(b, r), 0u) != sr::minifloat_bits<F, true>(b, r);
+    }
+    checks += 6;
+  }
+  std::printf("%s grid: %llu mismatches of %llu\n", name, mismatches, checks);
+  return mismatches;
+}
+
 int main() {
-  const unsigned long long bad = sweep<sr::F16>("F16") + sweep<sr::E4M3>("E4M3") + sweep<sr::E5M2>("E5M2");
+  const unsigned long long bad = sweep<sr::F16>("F16") + sweep<sr::E4M3>("E4M3") + sweep<sr::E5M2>("E5M2") +
+                                 sweep_fp8<sr::E4M3>("E4M3") + sweep_fp8<sr::E5M2>("E5M2");
   return bad != 0;
 }

@@ -4,7 +4,8 @@ tests/native/minifloat_fast.cpp compiles csrc/sr_math.h for the host, where
 sr::minifloat_bits_fast finishes with the integer nearest form instead of a
 hardware convert, and compares it with sr::minifloat_bits on every 257th
 FP32 input: nearest once, stochastic at the random values where the input's
-decision flips and at the extremes.  The exhaustive comparison including the
+decision flips and at the extremes.  It also checks sr::fp8_sr_grid_bits,
+the kernels' single-form FP8 stochastic rounding, the same way.  The exhaustive comparison including the
 hardware converts runs on the device (tests/test_gpu_minifloat_check.py).
 """
 
@@ -23,4 +24,5 @@ def test_minifloat_fast_bit_arithmetic_matches_the_integer_form(tmp_path):
     result = subprocess.run([str(binary)], capture_output=True, text=True, timeout=300)
     assert result.returncode == 0, result.stdout + result.stderr
     lines = result.stdout.strip().splitlines()
-    assert len(lines) == 3 and all(" 0 mismatches of 116" in line for line in lines), result.stdout
+    assert len(lines) == 5 and all(" 0 mismatches of " in line for line in lines), result.stdout
+    assert all(" 0 mismatches of 116" in line for line in lines[:3]), result.stdout
