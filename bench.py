@@ -590,6 +590,38 @@ def bandwidth_matrix(elements: int, reps: int, rounds: int):
     return n, rows
 
 
+# Gaps between consecutive stream bases for the placement sweep.
+PLACEMENT_GAPS = (0, 256, 4096, 65536, 1 << 20, 2 << 20, (2 << 20) + 4096, 3 << 20, 16 << 20)
+
+
+def stream_placements(elements: int, reps: int):
+    """Rate of the trivial kernel with the fused update's streams at several stream placements.
+
+    For the north star's streams (FP32 p/g, BF16 m/v) and the same with BF16
+    p/g: one allocation, each stream PLACEMENT_GAPS[i] bytes after the end of
+    the previous one (tests/native/stream_ceiling.hip, sr_stream_placements).
+    """
+    import ctypes
+
+    if not CEILING_LIBRARY.exists():
+        raise SystemExit(f"{CEILING_LIBRARY} is not built (tests/native/build_checks.py)")
+    lib = ctypes.CDLL(str(CEILING_LIBRARY))
+    lib.sr_stream_placements.restype = ctypes.c_int
+    lib.sr_stream_placements.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_int, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int,
+                                         ctypes.POINTER(ctypes.c_float)]
+    n = elements // 512 * 512
+    gaps = (ctypes.c_uint64 * len(PLACEMENT_GAPS))(*PLACEMENT_GAPS)
+    out = []
+    for name, widths, bpe in (("fp32_params", (4, 4, 2, 2), 20), ("bf16_params", (2, 2, 2, 2), 14)):
+        ms = (ctypes.c_float * len(PLACEMENT_GAPS))()
+        if lib.sr_stream_placements(n, *widths, reps, gaps, len(PLACEMENT_GAPS), ms) != 0:
+            raise SystemExit("sr_stream_placements failed")
+        out.append({"streams": name, "bytes_per_element": bpe,
+                    "gbps_by_gap": {str(g): bpe * n / t / 1e6 for g, t in zip(PLACEMENT_GAPS, ms)}})
+    return out
+
+
 def load_traffic(workload: str):
     """HBM bytes per launch from the committed rocprofv3 FETCH/WRITE summary, or None."""
     for path in sorted((ROOT / "profiles").glob(f"*_{workload}_hbm_traffic.md")):
@@ -645,13 +677,14 @@ def main():
     device = torch.device("cuda", 0)
     if spec["optimizer"] == "matrix":
         n, rows = bandwidth_matrix(sum(math.prod(s) for s in spec["shapes"]), args.steps, args.warmup)
+        placements = stream_placements(sum(math.prod(s) for s in spec["shapes"]), args.steps)
         print(json.dumps({
             "metric": "bandwidth of trivial-math stream variants at the north star's footprint, 1 MI355X",
             "value": rows[0]["best_gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "higher_is_better": True, "vs_baseline": None, "dtype": "u32",
             "data": "constant fill, XOR folds", "elements": n,
             "note": "steps = launches per variant per round, warmup = interleaved rounds",
-            "peak": HBM_PEAK_GBPS, "matrix": rows}), flush=True)
+            "peak": HBM_PEAK_GBPS, "matrix": rows, "placements": placements}), flush=True)
         return
     work = build(spec, device)
     step = work.step

@@ -38,13 +38,20 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 #define SR_LDS __attribute__((address_space(3)))
 
+#define SR_GLOBAL __attribute__((address_space(1)))
+
+// Addressing as the fused kernels address a tile: a workgroup-uniform tile
+// base plus the lane's 32-bit byte offset, in the global address space, each
+// store's offset in a fresh register (a shared one makes the compiler form
+// full 64-bit store addresses).
 template <class T>
-__device__ __forceinline__ T ld(const char* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
+__device__ __forceinline__ T ld(const char* tile, uint32_t offset) {
+  return __builtin_nontemporal_load((const SR_GLOBAL T*)(tile + offset));
 }
 template <class T>
-__device__ __forceinline__ void st(char* p, T v) {
-  __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+__device__ __forceinline__ void st(char* tile, uint32_t offset, T v) {
+  __asm__("" : "+v"(offset));
+  __builtin_nontemporal_store(v, (SR_GLOBAL T*)(tile + offset));
 }
 __device__ __forceinline__ uint32_t fold(u4 w) { return w.x ^ w.y ^ w.z ^ w.w; }
 __device__ __forceinline__ uint32_t fold(u2 w) { return w.x ^ w.y; }
@@ -71,27 +78,28 @@ template <int ROLE, int K>
 __global__ __launch_bounds__(kBlock) void seven_streams(Buffers b) {
   const uint32_t unit = unit_of(b.groups);
   if (unit >= b.groups) return;
-  const uint64_t first = static_cast<uint64_t>(unit) * K * kTile + threadIdx.x * kLanes;
+  const uint64_t first = static_cast<uint64_t>(unit) * K * kTile;
+  const uint32_t lane = threadIdx.x * kLanes;
   u4 wp[K], wg[K];
   u2 wm[K], wv[K];
   if constexpr (ROLE != WRITE_ONLY) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      const uint64_t i = first + static_cast<uint64_t>(k) * kTile;
-      wp[k] = ld<u4>(b.p + i * 4);
-      wg[k] = ld<u4>(b.g + i * 4);
-      wm[k] = ld<u2>(b.m + i * 2);
-      wv[k] = ld<u2>(b.v + i * 2);
+      const uint64_t t = first + static_cast<uint64_t>(k) * kTile;
+      wp[k] = ld<u4>(b.p + t * 4, lane * 4);
+      wg[k] = ld<u4>(b.g + t * 4, lane * 4);
+      wm[k] = ld<u2>(b.m + t * 2, lane * 2);
+      wv[k] = ld<u2>(b.v + t * 2, lane * 2);
     }
   }
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const uint64_t i = first + static_cast<uint64_t>(k) * kTile;
+    const uint64_t t = first + static_cast<uint64_t>(k) * kTile;
     if constexpr (ROLE == WRITE_ONLY) {
-      const uint32_t h = static_cast<uint32_t>(i) * 0x9E3779B9u;
-      st<u4>(b.p + i * 4, u4{h, h + 1, h + 2, h + 3});
-      st<u2>(b.m + i * 2, u2{h, h + 5});
-      st<u2>(b.v + i * 2, u2{h + 7, h});
+      const uint32_t h = static_cast<uint32_t>(t + lane) * 0x9E3779B9u;
+      st<u4>(b.p + t * 4, lane * 4, u4{h, h + 1, h + 2, h + 3});
+      st<u2>(b.m + t * 2, lane * 2, u2{h, h + 5});
+      st<u2>(b.v + t * 2, lane * 2, u2{h + 7, h});
     } else {
       const uint32_t h = fold(wp[k]) ^ fold(wg[k]) ^ fold(wm[k]) ^ fold(wv[k]);
       if constexpr (ROLE == READ_ONLY) {
@@ -99,9 +107,9 @@ __global__ __launch_bounds__(kBlock) void seven_streams(Buffers b) {
         // but the compiler cannot know, so the loads stay.
         if (h == b.groups * 7919u + 1u) b.sink[threadIdx.x & 15] = h;
       } else {
-        st<u4>(b.p + i * 4, wp[k] ^ h);
-        st<u2>(b.m + i * 2, wm[k] ^ h);
-        st<u2>(b.v + i * 2, wv[k] ^ h);
+        st<u4>(b.p + t * 4, lane * 4, wp[k] ^ h);
+        st<u2>(b.m + t * 2, lane * 2, wm[k] ^ h);
+        st<u2>(b.v + t * 2, lane * 2, wv[k] ^ h);
       }
     }
   }
@@ -121,35 +129,41 @@ template <int SHAPE>
 __global__ __launch_bounds__(kBlock) void stream_set(Buffers b) {
   const uint32_t unit = unit_of(b.groups);
   if (unit >= b.groups) return;
-  const uint64_t i = static_cast<uint64_t>(unit) * kTile + threadIdx.x * kLanes;
+  const uint64_t t = static_cast<uint64_t>(unit) * kTile;
+  const uint32_t l4 = threadIdx.x * kLanes * 4, l2 = threadIdx.x * kLanes * 2;
+  char* const p = b.p + t * 4;
+  char* const g = b.g + t * 4;
+  char* const m2 = b.m + t * 2;
+  char* const m4 = b.m + t * 4;
+  char* const v = b.v + t * 2;
   if constexpr (SHAPE == COPY_IN_PLACE) {
-    const u4 wp = ld<u4>(b.p + i * 4);
-    st<u4>(b.p + i * 4, wp ^ fold(wp));
+    const u4 wp = ld<u4>(p, l4);
+    st<u4>(p, l4, wp ^ fold(wp));
   } else if constexpr (SHAPE == COPY_TWO) {
-    const u4 wg = ld<u4>(b.g + i * 4);
-    st<u4>(b.p + i * 4, wg ^ fold(wg));
+    const u4 wg = ld<u4>(g, l4);
+    st<u4>(p, l4, wg ^ fold(wg));
   } else if constexpr (SHAPE == ONE_WRITTEN) {
-    const u4 wp = ld<u4>(b.p + i * 4), wg = ld<u4>(b.g + i * 4);
-    st<u4>(b.p + i * 4, wp ^ (fold(wp) ^ fold(wg)));
+    const u4 wp = ld<u4>(p, l4), wg = ld<u4>(g, l4);
+    st<u4>(p, l4, wp ^ (fold(wp) ^ fold(wg)));
   } else if constexpr (SHAPE == TWO_WRITTEN) {
-    const u4 wp = ld<u4>(b.p + i * 4), wg = ld<u4>(b.g + i * 4);
-    const u2 wm = ld<u2>(b.m + i * 2);
+    const u4 wp = ld<u4>(p, l4), wg = ld<u4>(g, l4);
+    const u2 wm = ld<u2>(m2, l2);
     const uint32_t h = fold(wp) ^ fold(wg) ^ fold(wm);
-    st<u4>(b.p + i * 4, wp ^ h);
-    st<u2>(b.m + i * 2, wm ^ h);
+    st<u4>(p, l4, wp ^ h);
+    st<u2>(m2, l2, wm ^ h);
   } else if constexpr (SHAPE == NO_GRADIENT) {
-    const u4 wp = ld<u4>(b.p + i * 4);
-    const u2 wm = ld<u2>(b.m + i * 2), wv = ld<u2>(b.v + i * 2);
+    const u4 wp = ld<u4>(p, l4);
+    const u2 wm = ld<u2>(m2, l2), wv = ld<u2>(v, l2);
     const uint32_t h = fold(wp) ^ fold(wm) ^ fold(wv);
-    st<u4>(b.p + i * 4, wp ^ h);
-    st<u2>(b.m + i * 2, wm ^ h);
-    st<u2>(b.v + i * 2, wv ^ h);
+    st<u4>(p, l4, wp ^ h);
+    st<u2>(m2, l2, wm ^ h);
+    st<u2>(v, l2, wv ^ h);
   } else {
     static_assert(SHAPE == MV_PAIRED, "unknown stream set");
-    const u4 wp = ld<u4>(b.p + i * 4), wg = ld<u4>(b.g + i * 4), wmv = ld<u4>(b.m + i * 4);
+    const u4 wp = ld<u4>(p, l4), wg = ld<u4>(g, l4), wmv = ld<u4>(m4, l4);
     const uint32_t h = fold(wp) ^ fold(wg) ^ fold(wmv);
-    st<u4>(b.p + i * 4, wp ^ h);
-    st<u4>(b.m + i * 4, wmv ^ h);
+    st<u4>(p, l4, wp ^ h);
+    st<u4>(m4, l4, wmv ^ h);
   }
 }
 
@@ -190,11 +204,12 @@ struct Staged {
   __device__ __forceinline__ void request(int k) const {
     char* s = slot(k);
     const uint64_t w0 = first + static_cast<uint64_t>(k) * kTile + wave * (kTile / 2);
-    __builtin_amdgcn_global_load_lds(b->p + (w0 + lane * 4) * 4, (SR_LDS void*)(s), 16, 0, 2);
-    __builtin_amdgcn_global_load_lds(b->g + (w0 + lane * 4) * 4, (SR_LDS void*)(s + 1024), 16, 0, 2);
+    const uint32_t offset = static_cast<uint32_t>(lane) * 16u;
+    __builtin_amdgcn_global_load_lds((const SR_GLOBAL void*)(b->p + w0 * 4 + offset), (SR_LDS void*)(s), 16, 0, 2);
+    __builtin_amdgcn_global_load_lds((const SR_GLOBAL void*)(b->g + w0 * 4 + offset), (SR_LDS void*)(s + 1024), 16, 0, 2);
     if (lane < 32) {
-      __builtin_amdgcn_global_load_lds(b->m + w0 * 2 + lane * 16, (SR_LDS void*)(s + 2048), 16, 0, 2);
-      __builtin_amdgcn_global_load_lds(b->v + w0 * 2 + lane * 16, (SR_LDS void*)(s + 2560), 16, 0, 2);
+      __builtin_amdgcn_global_load_lds((const SR_GLOBAL void*)(b->m + w0 * 2 + offset), (SR_LDS void*)(s + 2048), 16, 0, 2);
+      __builtin_amdgcn_global_load_lds((const SR_GLOBAL void*)(b->v + w0 * 2 + offset), (SR_LDS void*)(s + 2560), 16, 0, 2);
     }
   }
 
@@ -205,10 +220,11 @@ struct Staged {
     const u2 wm = *reinterpret_cast<const u2*>(s + 2048 + lane * 8);
     const u2 wv = *reinterpret_cast<const u2*>(s + 2560 + lane * 8);
     const uint32_t h = fold(wp) ^ fold(wg) ^ fold(wm) ^ fold(wv);
-    const uint64_t i = first + static_cast<uint64_t>(k) * kTile + (wave * 64 + lane) * kLanes;
-    st<u4>(b->p + i * 4, wp ^ h);
-    st<u2>(b->m + i * 2, wm ^ h);
-    st<u2>(b->v + i * 2, wv ^ h);
+    const uint64_t t = first + static_cast<uint64_t>(k) * kTile;
+    const uint32_t l = static_cast<uint32_t>(wave * 64 + lane) * kLanes;
+    st<u4>(b->p + t * 4, l * 4, wp ^ h);
+    st<u2>(b->m + t * 2, l * 2, wm ^ h);
+    st<u2>(b->v + t * 2, l * 2, wv ^ h);
   }
 
   template <int k>

@@ -4,7 +4,8 @@
 // streams of one fused-update launch: a parameter (FP32 or BF16) read and
 // written, a gradient read, and one or two states read and written, with the product's
 // tile shape (128 lanes x 4 elements), its XCD-chunked tile order
-// (sr_tile_order.h) and its non-temporal accesses.  Whatever rate this
+// (sr_tile_order.h), its addressing (a scalar tile base plus a 32-bit lane
+// offset) and its non-temporal accesses.  Whatever rate this
 // kernel reaches for n elements is what the memory system gives that access
 // pattern at that footprint; the fused kernels do strictly more work per
 // byte, so their rate over this one says how much of the reachable
@@ -43,15 +44,20 @@ __device__ __forceinline__ uint32_t fold(const word4& w) { return w.x ^ w.y ^ w.
 __device__ __forceinline__ uint32_t fold(const word2& w) { return w.x ^ w.y; }
 __device__ __forceinline__ uint32_t fold(uint32_t w) { return w; }
 
+// Addressing as the fused kernels address a tile: a workgroup-uniform tile
+// base (scalar registers) plus the lane's 32-bit byte offset, in the global
+// address space, and each store's offset in a fresh register (a shared one
+// makes the compiler form full 64-bit store addresses).
+#define SR_GLOBAL __attribute__((address_space(1)))
+
 template <int BYTES>
-__device__ __forceinline__ typename Access<BYTES>::type load(const void* base, uint64_t i) {
-  return __builtin_nontemporal_load(
-      reinterpret_cast<const typename Access<BYTES>::type*>(static_cast<const char*>(base) + i * BYTES));
+__device__ __forceinline__ typename Access<BYTES>::type load(const char* tile, uint32_t offset) {
+  return __builtin_nontemporal_load((const SR_GLOBAL typename Access<BYTES>::type*)(tile + offset));
 }
 template <int BYTES>
-__device__ __forceinline__ void store(void* base, uint64_t i, typename Access<BYTES>::type w) {
-  __builtin_nontemporal_store(
-      w, reinterpret_cast<typename Access<BYTES>::type*>(static_cast<char*>(base) + i * BYTES));
+__device__ __forceinline__ void store(char* tile, uint32_t offset, typename Access<BYTES>::type w) {
+  __asm__("" : "+v"(offset));
+  __builtin_nontemporal_store(w, (SR_GLOBAL typename Access<BYTES>::type*)(tile + offset));
 }
 
 // P, G, M, V: bytes per element of the parameter, the gradient and the two
@@ -61,22 +67,27 @@ template <int P, int G, int M, int V>
 __global__ __launch_bounds__(kBlock) void streams(void* p, const void* g, void* m, void* v, uint32_t tiles) {
   const uint32_t t = sr::tile_of(blockIdx.y * gridDim.x + blockIdx.x, tiles);
   if (t >= tiles) return;
-  const uint64_t i = static_cast<uint64_t>(t) * kTile + threadIdx.x * kLanes;
+  const uint64_t first = static_cast<uint64_t>(t) * kTile;
+  const uint32_t lane = threadIdx.x * kLanes;
+  char* tp = static_cast<char*>(p) + first * P;
+  const char* tg = static_cast<const char*>(g) + first * G;
+  char* tm = static_cast<char*>(m) + first * M;
+  char* tv = static_cast<char*>(v) + first * (V > 0 ? V : 1);
   // Every load is issued before any store, as in the fused kernels: the
   // pointers may alias as far as the compiler knows, so a load placed after
   // a store would wait for it.
-  auto wp = load<P>(p, i);
-  auto wg = load<G>(g, i);
-  auto wm = load<M>(m, i);
+  auto wp = load<P>(tp, lane * P);
+  auto wg = load<G>(tg, lane * G);
+  auto wm = load<M>(tm, lane * M);
   typename Access<(V > 0 ? V : 1)>::type wv{};
-  if constexpr (V > 0) wv = load<V>(v, i);
+  if constexpr (V > 0) wv = load<V>(tv, lane * V);
   const uint32_t h = fold(wg) ^ fold(wp) ^ fold(wm) ^ fold(wv);
   wp ^= h;
   wm ^= h;
   wv ^= h;
-  store<P>(p, i, wp);
-  store<M>(m, i, wm);
-  if constexpr (V > 0) store<V>(v, i, wv);
+  store<P>(tp, lane * P, wp);
+  store<M>(tm, lane * M, wm);
+  if constexpr (V > 0) store<V>(tv, lane * V, wv);
 }
 
 // The cast's pattern: 8 FP32 elements read and 8 narrower ones written per
@@ -91,19 +102,17 @@ __global__ __launch_bounds__(kCastBlock) void cast_streams(const void* x, void* 
   const uint32_t t = sr::tile_of(blockIdx.y * gridDim.x + blockIdx.x, tiles);
   if (t >= tiles) return;
   // The cast's lane layout: two groups of 4 elements a workgroup-width apart.
-  const uint64_t i0 = static_cast<uint64_t>(t) * kCastTile + threadIdx.x * kLanes;
-  const uint64_t i1 = i0 + kCastBlock * kLanes;
-  const word4 a = load<4>(x, i0), b = load<4>(x, i1);
+  const uint64_t first = static_cast<uint64_t>(t) * kCastTile;
+  const uint32_t i0 = threadIdx.x * kLanes, i1 = i0 + kCastBlock * kLanes;
+  const char* tx = static_cast<const char*>(x) + first * 4;
+  char* ty = static_cast<char*>(y) + first * OUT;
+  const word4 a = load<4>(tx, i0 * 4), b = load<4>(tx, i1 * 4);
   if constexpr (OUT == 2) {
-    __builtin_nontemporal_store(word2{(a.x >> 16) | (a.y & 0xFFFF0000u), (a.z >> 16) | (a.w & 0xFFFF0000u)},
-                                reinterpret_cast<word2*>(static_cast<char*>(y) + i0 * 2));
-    __builtin_nontemporal_store(word2{(b.x >> 16) | (b.y & 0xFFFF0000u), (b.z >> 16) | (b.w & 0xFFFF0000u)},
-                                reinterpret_cast<word2*>(static_cast<char*>(y) + i1 * 2));
+    store<2>(ty, i0 * 2, word2{(a.x >> 16) | (a.y & 0xFFFF0000u), (a.z >> 16) | (a.w & 0xFFFF0000u)});
+    store<2>(ty, i1 * 2, word2{(b.x >> 16) | (b.y & 0xFFFF0000u), (b.z >> 16) | (b.w & 0xFFFF0000u)});
   } else {
-    __builtin_nontemporal_store((a.x >> 24) | ((a.y >> 16) & 0xFF00u) | ((a.z >> 8) & 0xFF0000u) | (a.w & 0xFF000000u),
-                                reinterpret_cast<uint32_t*>(static_cast<char*>(y) + i0));
-    __builtin_nontemporal_store((b.x >> 24) | ((b.y >> 16) & 0xFF00u) | ((b.z >> 8) & 0xFF0000u) | (b.w & 0xFF000000u),
-                                reinterpret_cast<uint32_t*>(static_cast<char*>(y) + i1));
+    store<1>(ty, i0, (a.x >> 24) | ((a.y >> 16) & 0xFF00u) | ((a.z >> 8) & 0xFF0000u) | (a.w & 0xFF000000u));
+    store<1>(ty, i1, (b.x >> 24) | ((b.y >> 16) & 0xFF00u) | ((b.z >> 8) & 0xFF0000u) | (b.w & 0xFF000000u));
   }
 }
 
@@ -127,59 +136,113 @@ Kernel pick(int p, int g, int m, int v) {
   return nullptr;
 }
 
+// The placements the ceiling tries: gaps between consecutive stream bases in
+// one allocation.  Where the streams land relative to each other moves the
+// rate of this pattern by a few percent (bench.py --workload
+// bandwidth_matrix prints a sweep), so the ceiling is the best of several.
+constexpr uint64_t kCeilingGaps[] = {0, 4096, 65536, 16ull << 20};
+constexpr uint64_t kMaxGap = 16ull << 20;
+
+// Times the trivial kernel for one placement: streams p, g, m, v (widths
+// w[0..3], w[3] = 0 for one state) laid out from `slab` with `gap` bytes
+// after each (every base a multiple of 256 bytes).  Returns the milliseconds
+// per launch over `reps` launches after two untimed ones, or a negative
+// value on a HIP error.
+float time_placement(Kernel kernel, char* slab, const uint64_t (&bytes)[4], uint64_t gap, uint32_t tiles, int reps,
+                     hipEvent_t start, hipEvent_t stop) {
+  void* bases[4] = {nullptr, nullptr, nullptr, nullptr};
+  uint64_t at = 0;
+  for (int k = 0; k < 4; ++k) {
+    if (bytes[k] == 0) continue;
+    bases[k] = slab + at;
+    at += (bytes[k] + 255) / 256 * 256 + gap;
+  }
+  const sr::LaunchShape shape = sr::launch_shape(tiles, kBlock);
+  auto launch = [&] {
+    hipLaunchKernelGGL(kernel, dim3(shape.x, shape.y), dim3(kBlock), 0, nullptr, bases[0], bases[1], bases[2],
+                       bases[3], tiles);
+  };
+  launch();
+  launch();
+  if (hipGetLastError() != hipSuccess || hipEventRecord(start, nullptr) != hipSuccess) return -1.0f;
+  for (int r = 0; r < reps; ++r) launch();
+  float ms = 0.0f;
+  if (hipGetLastError() != hipSuccess || hipEventRecord(stop, nullptr) != hipSuccess ||
+      hipEventSynchronize(stop) != hipSuccess || hipEventElapsedTime(&ms, start, stop) != hipSuccess)
+    return -1.0f;
+  return ms / reps;
+}
+
+// Times `kernel` over n elements at each gap in gaps[0..count) (every gap at
+// most kMaxGap), writing milliseconds per launch to ms[0..count).  Returns 0,
+// or 2 for a HIP error (buffers are freed either way).
+int time_placements(Kernel kernel, uint64_t n, const int (&widths)[4], const uint64_t* gaps, int count, int reps,
+                    float* ms) {
+  const uint32_t tiles = static_cast<uint32_t>(n / kTile);
+  const uint64_t bytes[4] = {n * widths[0], n * widths[1], n * widths[2], n * widths[3]};
+  uint64_t total = 0;
+  for (uint64_t b : bytes) total += b ? (b + 255) / 256 * 256 + kMaxGap : 0;
+  char* slab = nullptr;
+  hipEvent_t start = nullptr, stop = nullptr;
+  int rc = 2;
+  do {
+    if (hipDeviceSynchronize() != hipSuccess) break;
+    if (hipMalloc(reinterpret_cast<void**>(&slab), total) != hipSuccess ||
+        hipMemset(slab, 0x3A, total) != hipSuccess)
+      break;
+    if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess) break;
+    bool failed = false;
+    for (int i = 0; i < count && !failed; ++i) {
+      ms[i] = time_placement(kernel, slab, bytes, gaps[i], tiles, reps, start, stop);
+      failed = ms[i] < 0.0f;
+    }
+    if (!failed) rc = 0;
+  } while (false);
+  if (start) (void)hipEventDestroy(start);
+  if (stop) (void)hipEventDestroy(stop);
+  (void)hipDeviceSynchronize();
+  if (slab) (void)hipFree(slab);
+  return rc;
+}
+
+bool valid_streams(uint64_t n, int reps) { return n != 0 && n % kTile == 0 && n / kTile <= 0x7FFFF000ull && reps >= 1; }
+
 }  // namespace
 
 // Average milliseconds per launch of the trivial kernel over n elements with
 // a parameter of p_bytes, a gradient of g_bytes and states of m_bytes and
 // v_bytes per element (v_bytes 0: one state), over `reps` launches after two
-// untimed ones.  Supported (p, g, m, v) patterns: FP32 parameters with
-// (4,2,2), (2,2,2), (4,1,2), (4,2,0), (4,4,4), (4,1,1), (4,4,0), (4,1,0);
-// BF16 parameters with (2,2,2), (2,1,2), (2,2,0).  n must be a positive
-// multiple of 512 with n / 512 <= 2^31 - 4096 (the fused launches' tile
-// limit); the grid is laid out as the fused launches lay it out
-// (sr::launch_shape).  Returns 0, or 1 for an unsupported argument, 2 for a
-// HIP error (buffers are freed either way).
+// untimed ones, at the best of the placements kCeilingGaps.  Supported
+// (p, g, m, v) patterns: FP32 parameters with (4,2,2), (2,2,2), (4,1,2),
+// (4,2,0), (4,4,4), (4,1,1), (4,4,0), (4,1,0); BF16 parameters with (2,2,2),
+// (2,1,2), (2,2,0).  n must be a positive multiple of 512 with n / 512 <=
+// 2^31 - 4096 (the fused launches' tile limit); the grid is laid out as the
+// fused launches lay it out (sr::launch_shape).  Returns 0, or 1 for an
+// unsupported argument, 2 for a HIP error (buffers are freed either way).
 extern "C" int sr_stream_ceiling_p(uint64_t n, int p_bytes, int g_bytes, int m_bytes, int v_bytes, int reps,
                                    float* avg_ms) {
   const Kernel kernel = pick(p_bytes, g_bytes, m_bytes, v_bytes);
-  if (!kernel || n == 0 || n % kTile || n / kTile > 0x7FFFF000ull || reps < 1 || !avg_ms) return 1;
-  const uint32_t tiles = static_cast<uint32_t>(n / kTile);
-  const sr::LaunchShape shape = sr::launch_shape(tiles, kBlock);
-  const size_t bytes[4] = {n * p_bytes, n * g_bytes, n * m_bytes, n * v_bytes};
-  void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
-  hipEvent_t start = nullptr, stop = nullptr;
-  int rc = 2;
-  do {
-    if (hipDeviceSynchronize() != hipSuccess) break;
-    bool ok = true;
-    for (int k = 0; k < 4 && ok; ++k) {
-      if (bytes[k] == 0) continue;
-      ok = hipMalloc(&buf[k], bytes[k]) == hipSuccess && hipMemset(buf[k], 0x3A, bytes[k]) == hipSuccess;
-    }
-    if (!ok) break;
-    if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess) break;
-    auto launch = [&] {
-      hipLaunchKernelGGL(kernel, dim3(shape.x, shape.y), dim3(kBlock), 0, nullptr, buf[0], buf[1], buf[2], buf[3],
-                         tiles);
-    };
-    launch();
-    launch();
-    if (hipGetLastError() != hipSuccess || hipEventRecord(start, nullptr) != hipSuccess) break;
-    for (int r = 0; r < reps; ++r) launch();
-    if (hipGetLastError() != hipSuccess || hipEventRecord(stop, nullptr) != hipSuccess ||
-        hipEventSynchronize(stop) != hipSuccess)
-      break;
-    float ms = 0.0f;
-    if (hipEventElapsedTime(&ms, start, stop) != hipSuccess) break;
-    *avg_ms = ms / reps;
-    rc = 0;
-  } while (false);
-  if (start) (void)hipEventDestroy(start);
-  if (stop) (void)hipEventDestroy(stop);
-  (void)hipDeviceSynchronize();
-  for (void* b : buf)
-    if (b) (void)hipFree(b);
-  return rc;
+  if (!kernel || !valid_streams(n, reps) || !avg_ms) return 1;
+  constexpr int kCount = sizeof(kCeilingGaps) / sizeof(kCeilingGaps[0]);
+  float ms[kCount];
+  const int rc = time_placements(kernel, n, {p_bytes, g_bytes, m_bytes, v_bytes}, kCeilingGaps, kCount, reps, ms);
+  if (rc != 0) return rc;
+  float best = ms[0];
+  for (float t : ms) best = t < best ? t : best;
+  *avg_ms = best;
+  return 0;
+}
+
+// The same kernel at caller-chosen placements: ms[i] receives the
+// milliseconds per launch with gaps[i] bytes (a multiple of 256, at most
+// 16 MiB) between consecutive stream bases; 1 <= count <= 64.
+extern "C" int sr_stream_placements(uint64_t n, int p_bytes, int g_bytes, int m_bytes, int v_bytes, int reps,
+                                    const uint64_t* gaps, int count, float* ms) {
+  const Kernel kernel = pick(p_bytes, g_bytes, m_bytes, v_bytes);
+  if (!kernel || !valid_streams(n, reps) || !gaps || !ms || count < 1 || count > 64) return 1;
+  for (int i = 0; i < count; ++i)
+    if (gaps[i] % 256 || gaps[i] > kMaxGap) return 1;
+  return time_placements(kernel, n, {p_bytes, g_bytes, m_bytes, v_bytes}, gaps, count, reps, ms);
 }
 
 // sr_stream_ceiling_p with an FP32 parameter.
