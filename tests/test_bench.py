@@ -58,3 +58,33 @@ def test_state_format_override_is_validated_before_anything_runs(value):
     result = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--state-format", value],
                             capture_output=True, text=True, timeout=300)
     assert result.returncode != 0 and "--state-format" in result.stderr
+
+
+def test_ceiling_helpers_refuse_bad_arguments_before_any_device_work():
+    """The placement sweep and the pattern ceiling check their arguments first (no GPU here)."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(bench.CEILING_LIBRARY))
+    lib.sr_stream_placements.restype = ctypes.c_int
+    lib.sr_stream_placements.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_int, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int,
+                                         ctypes.POINTER(ctypes.c_float)]
+    lib.sr_stream_ceiling_p.restype = ctypes.c_int
+    lib.sr_stream_ceiling_p.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
+    ms = (ctypes.c_float * 4)()
+
+    def placements(n, widths, gaps, reps=1):
+        array = (ctypes.c_uint64 * max(len(gaps), 1))(*gaps)
+        return lib.sr_stream_placements(n, *widths, reps, array, len(gaps), ms)
+
+    n = 512 * 1000
+    assert placements(n, (4, 4, 2, 2), [100]) == 1  # not a multiple of 256
+    assert placements(n, (4, 4, 2, 2), [(16 << 20) + 256]) == 1  # above 16 MiB
+    assert placements(n, (4, 4, 2, 2), []) == 1
+    assert placements(n + 1, (4, 4, 2, 2), [0]) == 1  # not whole tiles
+    assert placements(n, (4, 4, 3, 2), [0]) == 1  # no such pattern
+    assert placements(n, (4, 4, 2, 2), [0], reps=0) == 1
+    assert lib.sr_stream_ceiling_p(n, 2, 4, 2, 2, 1, ms) == 1
+    assert lib.sr_stream_ceiling_p(0, 4, 4, 2, 2, 1, ms) == 1
+    assert bench.PLACEMENT_GAPS[0] == 0 and all(g % 256 == 0 and g <= 16 << 20 for g in bench.PLACEMENT_GAPS)
