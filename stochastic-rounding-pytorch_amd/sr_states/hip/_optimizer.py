@@ -3,6 +3,7 @@
 from __future__ import annotations
 
 import math
+from bisect import bisect_left
 
 import torch
 
@@ -48,18 +49,26 @@ def validate_tensor_layout(tensors):
 
 
 def validate_no_overlap(spans):
-    """Sweep (start, end, written) byte spans of one device.
+    """Reject any byte a written span shares with another span of the same device.
 
-    Gradients are read-only and may share storage with each other; every span
-    the update writes must be disjoint from every other span.
+    ``spans`` holds (start, end, written) byte ranges.  Read-only ranges
+    (gradients) may share storage with each other.  Sorted by start, the
+    written ranges must each end before the next one begins; they are then
+    ordered by their ends too, so a read range [a, b) meets a written one
+    exactly when the last written range starting before b ends after a.
     """
-    max_end = max_write_end = 0
-    for start, end, write in sorted(spans):
-        if start < (max_end if write else max_write_end):
-            raise ValueError("parameter, gradient, and state must not overlap optimizer writes")
-        max_end = max(max_end, end)
-        if write:
-            max_write_end = max(max_write_end, end)
+    spans = list(spans)
+    written = sorted((start, end) for start, end, write in spans if write)
+    starts = [start for start, _ in written]
+    clash = any(end > next_start for (_, end), next_start in zip(written, starts[1:]))
+    for start, end, write in spans:
+        if clash:
+            break
+        if not write:
+            last = bisect_left(starts, end) - 1
+            clash = last >= 0 and written[last][1] > start
+    if clash:
+        raise ValueError("parameter, gradient, and state must not overlap optimizer writes")
 
 
 def validate_tensors(parameter, gradient, *states):

@@ -367,3 +367,31 @@ def test_reference_checkpoints_load_into_hip_optimizers(name):
                 assert torch.equal(bits(got), value)
             else:
                 assert got == value
+
+
+def test_overlap_rule_equals_the_pairwise_definition():
+    """Written byte ranges may share no byte with any other range; read ranges may share."""
+    import random
+
+    from sr_states.hip._optimizer import validate_no_overlap
+
+    def clashes(spans):
+        return any(
+            (w1 or w2) and s1 < e2 and s2 < e1
+            for i, (s1, e1, w1) in enumerate(spans)
+            for (s2, e2, w2) in spans[i + 1:]
+        )
+
+    rng = random.Random(7)
+    for _ in range(5000):
+        spans = []
+        for _ in range(rng.randint(1, 7)):
+            start = rng.randint(0, 40)
+            spans.append((start, start + rng.randint(1, 12), rng.random() < 0.6))
+        try:
+            validate_no_overlap(spans)
+            refused = False
+        except ValueError as error:
+            assert "must not overlap optimizer writes" in str(error)
+            refused = True
+        assert refused == clashes(spans), spans
