@@ -179,3 +179,18 @@ def test_c5_sgdm_fp16_twenty_steps(cuda):
     # (P(|N(0, 1e-2)| < 2^-14) = 0.49%, times the remaining 94%): 1.46%.
     tiny = (grads != 0) & (grads.abs() < 2.0**-14)
     assert 0.011 < float(tiny.float().mean()) < 0.018
+
+
+@pytest.mark.parametrize("workload", ["bf16_params_e4m3_bf16sr", "bf16_params_fp16sr"])
+def test_bf16_parameter_launches_full_size(cuda, workload):
+    """The arithmetic-heaviest launches at the north star's size, 3 steps.
+
+    BF16 parameters and gradients with an E4M3-SR first moment, or FP16-SR
+    moments: every element goes through the short square root and division
+    (with their library fallbacks where the moments or quotients are tiny)
+    and, for E4M3, the single-form FP8 encoder, at 3 M tiles.
+    """
+    spec = bench.WORKLOADS[workload]
+    assert spec["p_dtype"] == torch.bfloat16 and spec["g_dtype"] == torch.bfloat16
+    params, opt, samples = _run_optimizer_config(cuda, workload, 3, tensors=6, chunks=4)
+    assert len({index for index, *_ in samples}) == 6
