@@ -171,3 +171,32 @@ def test_functional_update_takes_local_tensors():
     with pytest.raises(TypeError, match="to_local"):
         hip_adamw_step_(p, p.clone(), m, m.clone(), lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
                         weight_decay=0.0, step=1)
+
+
+@pytest.mark.parametrize("update", ["adamw_step", "adamw_step_", "sgdm_step", "sgdm_step_"])
+def test_reference_functional_updates_take_local_tensors(update):
+    """sr_states.reference refuses DTensors as the fused single-tensor updates do."""
+    import sr_states.reference as functional
+
+    mesh = _mesh((2,), 1)
+    p = _dtensor(torch.zeros(4), mesh, (Shard(0),))
+    m = _dtensor(torch.zeros(4, dtype=torch.bfloat16), mesh, (Shard(0),))
+    if update.startswith("adamw"):
+        args = (p, p.clone(), m, m.clone())
+        options = dict(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, step=1)
+    else:
+        args = (p, p.clone(), m)
+        options = dict(lr=1e-3, momentum_factor=0.9)
+    with pytest.raises(TypeError, match="to_local"):
+        getattr(functional, update)(*args, **options)
+
+
+def test_eager_optimizers_reach_the_device_check_with_cpu_dtensors():
+    """AdamWReferenceSR takes DTensor parameters through their local shards; on CPU it stops there."""
+    from sr_states import AdamWReferenceSR
+
+    mesh = _mesh((2,), 0)
+    p = torch.nn.Parameter(_dtensor(torch.zeros(6, 2), mesh, (Shard(0),)))
+    p.grad = _dtensor(torch.ones(6, 2), mesh, (Shard(0),))
+    with pytest.raises(ValueError, match="run on the GPU"):
+        AdamWReferenceSR([p], lr=0.01).step()

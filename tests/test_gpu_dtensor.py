@@ -169,9 +169,25 @@ def _sgdm_fp16_sr(parameters):
     return sr_states.SGDMHip(parameters, lr=0.1, state_dtype=torch.float16, seed=13)
 
 
+def _adamw_reference_e4m3_bf16(parameters):
+    """The eager per-parameter optimizer: one launch per local shard."""
+    formats = {"exp_avg": sr_states.StateFormat(torch.float8_e4m3fn),
+               "exp_avg_sq": sr_states.StateFormat(torch.bfloat16)}
+    return sr_states.AdamWReferenceSR(parameters, lr=1e-3, seed=14, state_format=formats)
+
+
+def _sgdm_reference_fp16_sr(parameters):
+    return sr_states.SGDMReferenceSR(parameters, lr=0.1, state_dtype=torch.float16, seed=15)
+
+
 OPTIMIZERS = {
     "adamw_bf16_sr": (_adamw_bf16_sr, ("exp_avg", "exp_avg_sq"),
                       _adamw_oracle(11, [(torch.bfloat16, "stochastic")] * 2)),
+    "adamw_reference_e4m3_bf16": (_adamw_reference_e4m3_bf16, ("exp_avg", "exp_avg_sq"),
+                                  _adamw_oracle(14, [(torch.float8_e4m3fn, "stochastic"),
+                                                     (torch.bfloat16, "stochastic")])),
+    "sgdm_reference_fp16_sr": (_sgdm_reference_fp16_sr, ("momentum_buffer",),
+                               _sgdm_oracle(15, [(torch.float16, "stochastic")])),
     "adamw_e4m3_bf16": (_adamw_e4m3_bf16, ("exp_avg", "exp_avg_sq"),
                         _adamw_oracle(12, [(torch.float8_e4m3fn, "stochastic"), (torch.bfloat16, "stochastic")])),
     "sgdm_fp16_sr": (_sgdm_fp16_sr, ("momentum_buffer",), _sgdm_oracle(13, [(torch.float16, "stochastic")])),
@@ -181,7 +197,7 @@ OPTIMIZERS = {
 @pytest.mark.parametrize("mesh_shape, placements", MESHES)
 @pytest.mark.parametrize("kind", list(OPTIMIZERS))
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_fused_optimizers_update_each_shard_as_its_slice_of_the_whole(cuda, kind, mesh_shape, placements, dtype):
+def test_optimizers_update_each_shard_as_its_slice_of_the_whole(cuda, kind, mesh_shape, placements, dtype):
     make, names, oracle = OPTIMIZERS[kind]
     params, grads = _problem(cuda, seed=len(kind) + len(mesh_shape), dtype=dtype)
     full_params, full_opt = _run(make, params, grads, lambda t: t.clone())
