@@ -17,10 +17,24 @@ import torch
 
 import sr_states
 import sr_states.rounding as rounding_module
-from sr_states import AdamWHip, AdamWHipRN, SGDMHip, SGDMHipRN, StateFormat, cast, register_rounding
+from sr_states import (
+    AdamWHip,
+    AdamWHipRN,
+    AdamWReferenceRN,
+    AdamWReferenceSR,
+    SGDMHip,
+    SGDMHipRN,
+    SGDMReferenceRN,
+    SGDMReferenceSR,
+    StateFormat,
+    cast,
+    register_rounding,
+)
 from sr_states.rounding import validate_rounding
 
 CLASSES = [AdamWHip, SGDMHip]
+# The fused optimizers and the per-parameter ones share the host contract.
+ALL_CLASSES = [AdamWHip, SGDMHip, AdamWReferenceSR, SGDMReferenceSR]
 GOLDEN = Path(__file__).parent / "golden" / "reference_trajectories.pt"
 
 
@@ -51,7 +65,7 @@ def test_state_format_serialization_and_backends():
     assert StateFormat(torch.float8_e4m3fn).to_dict() == {"dtype": torch.float8_e4m3fn, "rounding": "stochastic"}
 
 
-@pytest.mark.parametrize("cls", CLASSES)
+@pytest.mark.parametrize("cls", ALL_CLASSES)
 def test_format_validation_and_group_overrides(cls):
     """tests/test_state_formats.py:103-134."""
     p, q = [torch.nn.Parameter(torch.ones(3)) for _ in range(2)]
@@ -86,7 +100,8 @@ def test_shorthand_single_and_dict_formats_serialize_identically():
     assert groups[0] == groups[1] == groups[2]
 
 
-@pytest.mark.parametrize("rn,sr", [(AdamWHipRN, AdamWHip), (SGDMHipRN, SGDMHip)])
+@pytest.mark.parametrize("rn,sr", [(AdamWHipRN, AdamWHip), (SGDMHipRN, SGDMHip),
+                                   (AdamWReferenceRN, AdamWReferenceSR), (SGDMReferenceRN, SGDMReferenceSR)])
 def test_rn_classes_force_nearest(rn, sr):
     """tests/test_state_formats.py:258-293 (host part)."""
     dtypes = (torch.float8_e4m3fn, torch.float8_e5m2)
@@ -212,7 +227,7 @@ def test_hip_optimizers_reject_reference_only_rules(cls):
         cls([torch.nn.Parameter(torch.ones(1))], lr=0.1, rounding="toward_zero")
 
 
-@pytest.mark.parametrize("cls", CLASSES)
+@pytest.mark.parametrize("cls", ALL_CLASSES)
 def test_group_overrides_and_checkpoints_require_registration(cls):
     """tests/test_rounding_registry.py:93-110."""
     p = torch.nn.Parameter(torch.ones(1))
@@ -253,7 +268,7 @@ def test_sgdm_rejects_invalid_options(kwargs, message):
 
 
 # -- checkpoints -------------------------------------------------------------------
-@pytest.mark.parametrize("cls", CLASSES)
+@pytest.mark.parametrize("cls", ALL_CLASSES)
 @pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("parameter_dtype", [torch.float32, torch.bfloat16])
 def test_checkpoint_keeps_state_precision(cls, state_dtype, parameter_dtype):
@@ -337,9 +352,10 @@ def test_legacy_group_keys_are_migrated():
     assert "state_format" not in old["param_groups"][0]
 
 
+@pytest.mark.parametrize("eager", [False, True], ids=["fused", "eager"])
 @pytest.mark.parametrize("name", ["adamw_mixed", "adamw_minifloat", "sgdm_mixed"])
-def test_reference_checkpoints_load_into_hip_optimizers(name):
-    """A state_dict written by the reference's eager optimizer loads unchanged."""
+def test_reference_checkpoints_load_into_hip_optimizers(name, eager):
+    """A state_dict written by the reference's eager optimizer loads unchanged, into either kind."""
     case = torch.load(GOLDEN, weights_only=True)["cases"][name]
     checkpoint = case["state_dict"]
     stream = io.BytesIO()
@@ -352,7 +368,10 @@ def test_reference_checkpoints_load_into_hip_optimizers(name):
     for group in case["groups"]:
         groups.append({"params": params[at: at + len(group["sizes"])]})
         at += len(group["sizes"])
-    cls = AdamWHip if case["kind"] == "adamw" else SGDMHip
+    if eager:
+        cls = AdamWReferenceSR if case["kind"] == "adamw" else SGDMReferenceSR
+    else:
+        cls = AdamWHip if case["kind"] == "adamw" else SGDMHip
     opt = cls(groups, lr=0.5, seed=1)
     opt.load_state_dict(checkpoint)
     for group, saved in zip(opt.param_groups, checkpoint["param_groups"]):
