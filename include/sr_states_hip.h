@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SR_ABI_VERSION 4
+#define SR_ABI_VERSION 5
 
 /* Storage dtypes (torch.float32, bfloat16, float16, float8_e4m3fn,
  * float8_e5m2).  The set mirrors the built-in rounding table of the
@@ -146,6 +146,17 @@ uint32_t sr_state_key(uint32_t key, uint32_t state_index);
  * arithmetic is sr_states/rounding.py:97-142. */
 int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule,
             uint32_t seed, uint32_t offset, int block_size, void* stream);
+
+/* lower[i], upper[i] = the two `dtype` values stochastic rounding chooses
+ * between for x[i], ordered, for i < n; both the nearest-even value when
+ * x[i] is representable, Inf or NaN.  Saturating FP8 formats clamp |x| to
+ * their maximum first; FP16 brackets finite magnitudes above 65504 by 65504
+ * and Inf.  dtype: SR_BF16, SR_F16, SR_E4M3 or SR_E5M2.  x: contiguous
+ * FP32; lower, upper: contiguous storage of `dtype`, disjoint from x.
+ * Replaces `bf16_neighbors` (sr_states/_bf16.py:77-101) and
+ * `minifloat_neighbors` (sr_states/_minifloat.py:73-99), which
+ * sr_states/reference/rounding.py:1-9 exports. */
+int sr_neighbors(const void* x, void* lower, void* upper, int64_t n, int dtype, void* stream);
 
 /* ---- fused AdamW ------------------------------------------------------ */
 

@@ -36,6 +36,7 @@ struct Tables {
   sr::KernelTableAdamW adamw{};
   sr::KernelTableSgdm sgdm{};
   sr::KernelTableCast cast{};
+  sr::KernelTableNeighbors neighbors{};
 };
 
 const Tables& tables() {
@@ -52,6 +53,7 @@ const Tables& tables() {
     sr::register_adamw_m8(r.adamw);
     sr::register_sgdm(r.sgdm);
     sr::register_cast(r.cast);
+    sr::register_neighbors(r.neighbors);
     return r;
   }();
   return t;
@@ -247,6 +249,26 @@ int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule, uint32_t see
   a.vector_ok = aligned16(x) && aligned16(y);
   if (int rc = tiles_for(n, block_size, sr::kCastLaneElements, &a.total_tiles)) return rc;
   return launch(tables().cast[enc], block_size, a.total_tiles, &a, stream);
+}
+
+int sr_neighbors(const void* x, void* lower, void* upper, int64_t n, int dtype, void* stream) {
+  if (dtype != SR_BF16 && dtype != SR_F16 && dtype != SR_E4M3 && dtype != SR_E5M2)
+    return fail(SR_ERR_ARGUMENT, "neighbors support BF16, FP16, E4M3 and E5M2, not dtype %d", dtype);
+  if (n < 0) return fail(SR_ERR_ARGUMENT, "negative element count");
+  if (n == 0) return SR_OK;
+  if (!x || !lower || !upper) return fail(SR_ERR_ARGUMENT, "null pointer");
+  sr::NeighborArgs a{static_cast<const float*>(x), lower, upper, n};
+  // Enough workgroups to fill the chip; the kernel's grid-stride loop covers
+  // any n with them.
+  constexpr int64_t kMaxGroups = 8192;
+  const int64_t groups = (n + sr::kNeighborBlock - 1) / sr::kNeighborBlock;
+  void* args[] = {&a};
+  const hipError_t err =
+      hipLaunchKernel(tables().neighbors[state_enc(dtype, SR_NEAREST)],
+                      dim3(static_cast<uint32_t>(groups < kMaxGroups ? groups : kMaxGroups)),
+                      dim3(sr::kNeighborBlock), args, 0, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return hip_fail(err, "hipLaunchKernel");
+  return SR_OK;
 }
 
 int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n, int p_dtype, int g_dtype,

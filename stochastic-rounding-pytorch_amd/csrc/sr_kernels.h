@@ -445,12 +445,37 @@ __global__ __launch_bounds__(kMaxBlock) void cast_kernel(const CastArgs a) {
   }
 }
 
+// Ordered neighbours of each FP32 input in the format of ENC (one of the
+// nearest encodings BF16_RN, F16_RN, E4M3_RN, E5M2_RN), a checking helper
+// (sr_states/_bf16.py:77-101, sr_states/_minifloat.py:73-99).  A grid-stride
+// loop: every lane leaves once its index passes n, whatever the grid.
+struct NeighborArgs {
+  const float* x;
+  void* lower;
+  void* upper;
+  int64_t n;
+};
+
+constexpr int kNeighborBlock = 256;
+
+template <int ENC>
+__global__ __launch_bounds__(kNeighborBlock) void neighbors_kernel(const NeighborArgs a) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.n; i += stride) {
+    uint32_t lower, upper;
+    neighbor_bits<ENC>(load1<ENC_F32>(a.x, i), lower, upper);
+    store1<ENC>(a.lower, i, lower);
+    store1<ENC>(a.upper, i, upper);
+  }
+}
+
 // Kernel tables (host stub addresses), filled by the instantiating units.
 // Index order: [param enc][grad enc][state enc...]; param/grad enc is 0 for
 // FP32 and 1 for BF16.
 using KernelTableAdamW = const void* [2][2][ENC_COUNT][ENC_COUNT];
 using KernelTableSgdm = const void* [2][2][ENC_COUNT];
 using KernelTableCast = const void* [ENC_COUNT];
+using KernelTableNeighbors = const void* [ENC_COUNT];  // nearest encodings only
 
 void register_adamw_m0(KernelTableAdamW&);
 void register_adamw_m1(KernelTableAdamW&);
@@ -463,5 +488,6 @@ void register_adamw_m7(KernelTableAdamW&);
 void register_adamw_m8(KernelTableAdamW&);
 void register_sgdm(KernelTableSgdm&);
 void register_cast(KernelTableCast&);
+void register_neighbors(KernelTableNeighbors&);
 
 }  // namespace sr

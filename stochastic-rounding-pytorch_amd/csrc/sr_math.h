@@ -329,6 +329,80 @@ SR_HD uint32_t minifloat_encode(uint32_t b, uint32_t hash) {
 #endif
 }
 
+// ---------------------------------------------------------------------------
+// Ordered neighbours: for each FP32 input, the two storage values that
+// stochastic rounding chooses between, lower <= x <= upper.  A checking
+// helper beside the encoders, not used by the updates.
+// ---------------------------------------------------------------------------
+
+// BF16 (sr_states/_bf16.py:77-101).  Dropping the low 16 bits moves toward
+// zero, and one more in the truncated BF16 word moves away from zero for
+// either sign (from the largest finite magnitude to Inf).  Inputs BF16
+// represents, Inf and NaN give their nearest-even conversion twice.
+SR_HD void bf16_neighbor_bits(uint32_t b, uint32_t& lower, uint32_t& upper) {
+  if ((b & 0xFFFFu) == 0u || (b & 0x7F800000u) == 0x7F800000u) {
+    lower = upper = bf16_rn_bits(b);
+    return;
+  }
+  const uint32_t toward = b >> 16;
+  const uint32_t away = toward + 1u;
+  const bool negative = (b >> 31) != 0u;
+  lower = negative ? away : toward;
+  upper = negative ? toward : away;
+}
+
+// The minifloat formats after their saturation policy
+// (sr_states/_minifloat.py:73-99).  With q and the spacing of
+// minifloat_bits, the value toward zero is q * spacing, whose encoding is
+// ((e - EMIN) << M) + q, and the one away from zero one encoding further
+// unless x lies on the grid: every nonzero remainder counts, however small,
+// also where the stochastic rule's 24-bit threshold is 0.  Saturating
+// formats clamp |x| (Inf included) to the maximum first.  FP16 brackets
+// finite magnitudes above its maximum by the maximum and Inf, and keeps
+// Inf.  NaN gives F's NaN twice.
+template <class F>
+SR_HD void minifloat_neighbor_bits(uint32_t b, uint32_t& lower, uint32_t& upper) {
+  const uint32_t sign = (b >> 31) << (F::kWidth - 1);
+  uint32_t a = b & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) {
+    lower = upper = F::kNan | sign;
+    return;
+  }
+  if (F::kSat) a = a < F::kMaxBits ? a : F::kMaxBits;
+  uint32_t toward, away;
+  if (!F::kSat && a > F::kMaxBits) {
+    toward = a == 0x7F800000u ? F::kInf : F::kInf - 1u;  // Inf, or the largest finite
+    away = F::kInf;
+  } else {
+    const int E = static_cast<int>(a >> 23);
+    const uint32_t sig = E ? ((a & 0x007FFFFFu) | 0x00800000u) : a;
+    const int e_raw = (E ? E : 1) - 127;
+    const int e = (E - 127) > F::kEmin ? (E - 127) : F::kEmin;
+    const int s = 23 - F::kM + (e - e_raw);  // >= 23 - M
+    const uint32_t q = s < 32 ? sig >> s : 0u;
+    const bool inexact = s < 32 ? (sig & ((1u << s) - 1u)) != 0u : sig != 0u;
+    toward = (static_cast<uint32_t>(e - F::kEmin) << F::kM) + q;
+    away = toward + (inexact ? 1u : 0u);
+  }
+  const bool negative = sign != 0u;
+  lower = (negative ? away : toward) | sign;
+  upper = (negative ? toward : away) | sign;
+}
+
+template <int ENC>
+SR_HD void neighbor_bits(uint32_t b, uint32_t& lower, uint32_t& upper) {
+  if constexpr (ENC == ENC_BF16_RN) {
+    bf16_neighbor_bits(b, lower, upper);
+  } else if constexpr (ENC == ENC_F16_RN) {
+    minifloat_neighbor_bits<F16>(b, lower, upper);
+  } else if constexpr (ENC == ENC_E4M3_RN) {
+    minifloat_neighbor_bits<E4M3>(b, lower, upper);
+  } else {
+    static_assert(ENC == ENC_E5M2_RN, "neighbours exist for BF16, FP16, E4M3 and E5M2");
+    minifloat_neighbor_bits<E5M2>(b, lower, upper);
+  }
+}
+
 // Encode an FP32 value into the storage bits of `ENC` with the counter's
 // hash.  The hash is only evaluated for stochastic encodings.
 template <int ENC>

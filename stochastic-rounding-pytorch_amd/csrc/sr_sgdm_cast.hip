@@ -1,4 +1,4 @@
-// Momentum-SGD and cast kernel instantiations.
+// Momentum-SGD, cast and neighbour kernel instantiations.
 #include <utility>
 
 #include "sr_kernels.h"
@@ -29,5 +29,12 @@ void register_sgdm(KernelTableSgdm& t) {
 }
 
 void register_cast(KernelTableCast& t) { fill_cast(t, std::make_integer_sequence<int, ENC_COUNT>{}); }
+
+void register_neighbors(KernelTableNeighbors& t) {
+  t[ENC_BF16_RN] = reinterpret_cast<const void*>(&neighbors_kernel<ENC_BF16_RN>);
+  t[ENC_F16_RN] = reinterpret_cast<const void*>(&neighbors_kernel<ENC_F16_RN>);
+  t[ENC_E4M3_RN] = reinterpret_cast<const void*>(&neighbors_kernel<ENC_E4M3_RN>);
+  t[ENC_E5M2_RN] = reinterpret_cast<const void*>(&neighbors_kernel<ENC_E5M2_RN>);
+}
 
 }  // namespace sr

@@ -17,7 +17,7 @@ import numpy as np
 import torch  # noqa: F401  (load torch's HIP runtime before the library)
 
 LIBRARY_PATH = Path(__file__).with_name("libsr_states_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 # Elements per lane of a launch (SR_LANE_ELEMENTS / _NARROW); lane_elements()
 # gives the width of a particular launch.
 LANE_ELEMENTS, LANE_ELEMENTS_NARROW = 4, 8
@@ -88,6 +88,7 @@ SIGNATURES = {
     "sr_update_key": (_u32, [_u64, _u64, _u32]),
     "sr_state_key": (_u32, [_u32, _u32]),
     "sr_cast": (_int, [_vp, _vp, _i64, _int, _int, _u32, _u32, _int, _vp]),
+    "sr_neighbors": (_int, [_vp, _vp, _vp, _i64, _int, _vp]),
     "sr_adamw_step": (
         _int,
         [_vp, _vp, _vp, _vp, _i64, _int, _int, _int, _int, _int, _int,

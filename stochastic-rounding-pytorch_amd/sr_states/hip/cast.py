@@ -52,6 +52,30 @@ def native_cast(x, *, dtype, rule, seed=0, offset=0, threads=_DEFAULT_THREADS, o
     return output
 
 
+NEIGHBOR_DTYPES = (torch.bfloat16, torch.float16, torch.float8_e4m3fn, torch.float8_e5m2)
+
+
+def native_neighbors(x, dtype):
+    """(lower, upper): the ordered ``dtype`` neighbours of contiguous GPU FP32 ``x``."""
+    if x.device.type != "cuda":
+        raise ValueError(f"sr_states neighbors run on the GPU; got a {x.device.type} tensor")
+    validate_device(x.device)
+    lower = torch.empty(x.shape, dtype=dtype, device=x.device)
+    upper = torch.empty(x.shape, dtype=dtype, device=x.device)
+    if x.numel():
+        with torch.cuda.device(x.device):
+            _lib.call(
+                "sr_neighbors",
+                x.data_ptr(),
+                lower.data_ptr(),
+                upper.data_ptr(),
+                x.numel(),
+                _lib.DTYPE_CODES[dtype],
+                _lib.stream_handle(x.device),
+            )
+    return lower, upper
+
+
 def check_out(x, out, dtype):
     """``out`` for a cast of ``x`` to ``dtype``: contiguous, same shape and device, disjoint.
 

@@ -1,9 +1,11 @@
-"""Seeded input sets shared by the CPU and GPU tests.
+"""Seeded input sets and enumerated neighbours shared by the CPU and GPU tests.
 
-They restate the reference's own test inputs: the cast-check cases
+The inputs restate the reference's own test inputs: the cast-check cases
 (benchmarks/cast_checks.py:10-67), the minifloat boundary sets
 (tests/test_minifloat.py:16-52) and the dyadic optimizer gradients
-(tests/test_rng_streams.py:33-38).
+(tests/test_rng_streams.py:33-38).  ``bf16_bracket`` and
+``oracle_neighbors`` find the neighbours of FP32 inputs by enumerating the
+target format, independently of any rounding formula.
 """
 
 from __future__ import annotations
@@ -73,3 +75,35 @@ def rn_midpoint_words() -> torch.Tensor:
 def dyadic_gradient(n: int = 1031) -> torch.Tensor:
     """1 + i/2048: FP32 AdamW/SGDM proposals from it are exact."""
     return 1.0 + torch.arange(n, dtype=torch.float32) / 2048
+
+
+def bf16_bracket(x: torch.Tensor):
+    """Independent BF16 neighbours of finite FP32 x by enumeration around RN(x)."""
+    rn = x.to(torch.bfloat16).view(torch.int16).to(torch.int32)
+    candidates = torch.stack([rn - 1, rn, rn + 1]).to(torch.int16).view(torch.bfloat16).float()
+    xf = x[None, :]
+    below = torch.where(candidates <= xf, candidates, torch.full_like(candidates, -float("inf")))
+    above = torch.where(candidates >= xf, candidates, torch.full_like(candidates, float("inf")))
+    # Across zero the integer neighbours of RN(x) are on the far side: sign-aware fix.
+    return below.max(0).values, above.min(0).values
+
+
+def oracle_neighbors(x, dtype):
+    """Enumerated-grid neighbours after saturation (tests/test_minifloat.py:55-74)."""
+    grid = positive_grid(dtype)
+    a = x.abs()
+    saturate = dtype != torch.float16
+    if saturate:
+        a = a.clamp_max(grid[-1].item())
+    index = torch.searchsorted(grid, a)
+    upper = grid[index.clamp_max(grid.numel() - 1)]
+    exact = upper == a
+    lower = torch.where(exact, upper, grid[(index - 1).clamp(0, grid.numel() - 1)])
+    if not saturate:
+        upper = torch.where(a > grid[-1], float("inf"), upper)
+        lower = torch.where(torch.isinf(a), float("inf"), lower)
+    lo = torch.copysign(torch.where(torch.signbit(x), upper, lower), x)
+    hi = torch.copysign(torch.where(torch.signbit(x), lower, upper), x)
+    lo = torch.where(torch.isnan(x), x, lo)
+    hi = torch.where(torch.isnan(x), x, hi)
+    return torch.minimum(lo, hi), torch.maximum(lo, hi)

@@ -31,6 +31,7 @@ def test_header_declares_the_expected_surface():
             "sr_update_key",
             "sr_state_key",
             "sr_cast",
+            "sr_neighbors",
             "sr_adamw_step",
             "sr_adamw_multi",
             "sr_adamw_multi_noalloc",
@@ -72,6 +73,12 @@ def test_invalid_arguments_fail_before_any_device_work():
     assert lib.sr_cast(None, None, 16, 1, 1, 0, 0, 100, None) == 1
     assert b"block size" in lib.sr_last_error()
     assert lib.sr_cast(None, None, 0, 1, 1, 0, 0, 256, None) == 0  # empty: nothing to do
+    assert lib.sr_neighbors(None, None, None, 16, 0, None) == 1  # FP32 has no neighbours
+    assert b"neighbors support" in lib.sr_last_error()
+    assert lib.sr_neighbors(None, None, None, 16, 3, None) == 1
+    assert b"null pointer" in lib.sr_last_error()
+    assert lib.sr_neighbors(None, None, None, -1, 3, None) == 1
+    assert lib.sr_neighbors(None, None, None, 0, 3, None) == 0  # empty: nothing to do
     hp = _lib.AdamWHparams()
     assert lib.sr_adamw_step(None, None, None, None, 8, 2, 0, 1, 1, 1, 1, ctypes.byref(hp), 0, 0, 256, None) == 1
     assert b"FP32 or BF16" in lib.sr_last_error()

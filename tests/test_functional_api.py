@@ -3,7 +3,7 @@
 The reference exports ``AdamWReferenceSR/RN`` and ``SGDMReferenceSR/RN`` at
 the top level (sr_states/__init__.py:3-17) and the functional updates in
 ``sr_states.reference`` (reference/adamw.py:12-127, reference/sgd.py:12-84,
-reference/rounding.py:12-14).  Here they run the HIP kernels, so on a CPU
+reference/rounding.py:1-14).  Here they run the HIP kernels, so on a CPU
 tensor they raise before any work instead of computing.
 """
 
@@ -103,6 +103,25 @@ def test_cpu_tensors_are_refused_by_sgdm(update):
 def test_stochastic_round_bf16_refuses_cpu_input():
     with pytest.raises(ValueError, match="on the GPU"):
         functional.stochastic_round_bf16(torch.zeros(4), seed=1)
+
+
+def test_neighbor_helpers_keep_the_reference_names_and_errors():
+    """reference/rounding.py:1-9 re-exports them; _bf16.py:24-26 and _minifloat.py:79-82 raise."""
+    from sr_states.reference.rounding import bf16_neighbors, minifloat_neighbors
+
+    assert functional.bf16_neighbors is bf16_neighbors
+    assert functional.minifloat_neighbors is minifloat_neighbors
+    assert {"bf16_neighbors", "cast", "minifloat_neighbors", "stochastic_round_bf16"} <= set(functional.__all__)
+    with pytest.raises(TypeError, match="expected torch.float32 input, got torch.float64"):
+        bf16_neighbors(torch.zeros(4, dtype=torch.float64))
+    with pytest.raises(TypeError, match="expected torch.float32 input"):
+        minifloat_neighbors(torch.zeros(4, dtype=torch.bfloat16), dtype=torch.float16)
+    with pytest.raises(ValueError, match="neighbors supports E4M3, E5M2, and FP16"):
+        minifloat_neighbors(torch.zeros(4), dtype=torch.bfloat16)
+    for call in (lambda: bf16_neighbors(torch.zeros(4)),
+                 lambda: minifloat_neighbors(torch.zeros(4), dtype=torch.float8_e5m2)):
+        with pytest.raises(ValueError, match="on the GPU"):
+            call()
 
 
 def test_argument_errors_come_before_device_checks():

@@ -17,8 +17,10 @@ import pytest
 import torch
 from _cases import (
     all_values,
+    bf16_bracket,
     boundary_inputs,
     cast_cases,
+    oracle_neighbors,
     positive_grid,
     random_words,
     rn_midpoint_words,
@@ -48,17 +50,6 @@ def test_c_and_torch_oracles_agree(dtype, rounding):
 # ---------------------------------------------------------------------------
 # BF16 stochastic rounding (sr_states/_bf16.py:37-74)
 # ---------------------------------------------------------------------------
-def bf16_bracket(x: torch.Tensor):
-    """Independent BF16 neighbours of finite FP32 x by enumeration around RN(x)."""
-    rn = x.to(torch.bfloat16).view(torch.int16).to(torch.int32)
-    candidates = torch.stack([rn - 1, rn, rn + 1]).to(torch.int16).view(torch.bfloat16).float()
-    xf = x[None, :]
-    below = torch.where(candidates <= xf, candidates, torch.full_like(candidates, -float("inf")))
-    above = torch.where(candidates >= xf, candidates, torch.full_like(candidates, float("inf")))
-    # Across zero the integer neighbours of RN(x) are on the far side: sign-aware fix.
-    return below.max(0).values, above.min(0).values
-
-
 def test_bf16_sr_output_is_a_neighbour_and_exact_values_are_fixed():
     gen = torch.Generator().manual_seed(123)
     x = torch.cat([torch.randn(20_000, generator=gen) * 100, torch.randn(20_000, generator=gen) * 1e-30])
@@ -138,27 +129,6 @@ def test_bf16_sr_is_unbiased_statistically():
 # ---------------------------------------------------------------------------
 # Minifloats (sr_states/_minifloat.py:10-70)
 # ---------------------------------------------------------------------------
-def oracle_neighbors(x, dtype):
-    """Enumerated-grid neighbours after saturation (tests/test_minifloat.py:55-74)."""
-    grid = positive_grid(dtype)
-    a = x.abs()
-    saturate = dtype != torch.float16
-    if saturate:
-        a = a.clamp_max(grid[-1].item())
-    index = torch.searchsorted(grid, a)
-    upper = grid[index.clamp_max(grid.numel() - 1)]
-    exact = upper == a
-    lower = torch.where(exact, upper, grid[(index - 1).clamp(0, grid.numel() - 1)])
-    if not saturate:
-        upper = torch.where(a > grid[-1], float("inf"), upper)
-        lower = torch.where(torch.isinf(a), float("inf"), lower)
-    lo = torch.copysign(torch.where(torch.signbit(x), upper, lower), x)
-    hi = torch.copysign(torch.where(torch.signbit(x), lower, upper), x)
-    lo = torch.where(torch.isnan(x), x, lo)
-    hi = torch.where(torch.isnan(x), x, hi)
-    return torch.minimum(lo, hi), torch.maximum(lo, hi)
-
-
 @pytest.mark.parametrize("dtype", MINIFLOATS)
 @pytest.mark.parametrize("rounding", RULES)
 def test_every_finite_encoding_is_fixed(dtype, rounding):
@@ -260,10 +230,21 @@ def test_round_up_probability(dtype):
 def test_oracle_bf16_neighbors_match_enumeration():
     """sr_oracle.bf16_neighbors (sr_states/_bf16.py:77-101) against enumeration."""
     gen = torch.Generator().manual_seed(5)
-    x = torch.cat([torch.randn(20_000, generator=gen) * 100, torch.tensor([1.5, -2.0, 0.0])])
+    words = random_words(50_000, 6)
+    boundary = torch.tensor([0x00000001, 0x00008000, 0x0000FFFF, 0x00010000, 0x3F807FFF, 0x3F808000,
+                             0x3F808001, 0x7F7F7FFF, 0x7F7F8000, 0x7F7FFFFF], dtype=torch.int64)
+    boundary = torch.cat((boundary, boundary | 0x80000000)).to(torch.int32).view(torch.float32)
+    x = torch.cat([torch.randn(20_000, generator=gen) * 100, torch.randn(20_000, generator=gen) * 1e-39,
+                   torch.tensor([1.5, -2.0, 0.0, -0.0]), boundary, words[torch.isfinite(words)]])
     lower, upper = sr_oracle.bf16_neighbors(x)
     lo, hi = bf16_bracket(x)
     assert torch.equal(lower.float(), lo) and torch.equal(upper.float(), hi)
+    assert torch.equal(torch.signbit(lower.float()), torch.signbit(x))
+    assert torch.equal(torch.signbit(upper.float()), torch.signbit(x))
+    special = torch.tensor([float("inf"), -float("inf"), float("nan")])
+    lower, upper = sr_oracle.bf16_neighbors(special)
+    assert_bits_or_nan(lower, special.to(torch.bfloat16))
+    assert_bits_or_nan(upper, special.to(torch.bfloat16))
 
 
 @pytest.mark.parametrize("dtype", MINIFLOATS)
