@@ -631,18 +631,42 @@ def load_traffic(workload: str):
     return None
 
 
+def positive_int(text: str) -> int:
+    """argparse type: an integer of at least 1."""
+    value = int(text)
+    if value < 1:
+        raise argparse.ArgumentTypeError(f"{text} is not a positive integer")
+    return value
+
+
+def nonnegative_int(text: str) -> int:
+    """argparse type: an integer of at least 0."""
+    value = int(text)
+    if value < 0:
+        raise argparse.ArgumentTypeError(f"{text} is not a nonnegative integer")
+    return value
+
+
+def positive_float(text: str) -> float:
+    """argparse type: a finite number above 0."""
+    value = float(text)
+    if not math.isfinite(value) or value <= 0:
+        raise argparse.ArgumentTypeError(f"{text} is not a positive number")
+    return value
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=None,
+    parser.add_argument("--gpus", type=positive_int, default=1)
+    parser.add_argument("--steps", type=positive_int, default=None,
                         help="timed steps (default: the workload's, 100 for the north star)")
-    parser.add_argument("--warmup", type=int, default=None,
+    parser.add_argument("--warmup", type=nonnegative_int, default=None,
                         help="untimed warmup steps (default: the workload's, 25 for the north star)")
     parser.add_argument("--workload", choices=sorted(WORKLOADS), default="north_star")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-ceiling", action="store_true",
                         help="skip the access-pattern ceiling measurement")
-    parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument("--cpu-seconds", type=positive_float, default=12.0)
     parser.add_argument("--state-format", default=None, metavar="DTYPE/RULE",
                         help="store every state of the workload in this format instead, e.g. "
                              "float8_e4m3fn/stochastic (the reference's nine policies: "
@@ -676,6 +700,8 @@ def main():
         args.steps = spec.get("steps", 100)
     device = torch.device("cuda", 0)
     if spec["optimizer"] == "matrix":
+        if args.warmup < 1:
+            raise SystemExit("--workload bandwidth_matrix takes --warmup as its number of rounds: at least 1")
         n, rows = bandwidth_matrix(sum(math.prod(s) for s in spec["shapes"]), args.steps, args.warmup)
         placements = stream_placements(sum(math.prod(s) for s in spec["shapes"]), args.steps)
         print(json.dumps({

@@ -1,9 +1,11 @@
-"""bench.py's contract on the CPU: workloads, byte accounting and the one-GPU rule.
+"""bench.py's contract on the CPU: workloads, byte accounting, arguments, validation.
 
 The timed run needs a GPU (the round-end driver runs it); here the
 workload table, the algorithmic bytes per element (the reference's traffic
-model, benchmarks/bench_states.py:65-70, extended to mixed widths) and the
-refusal of more than one GPU are checked without one.
+model, benchmarks/bench_states.py:65-70, extended to mixed widths), the
+refusal of more than one GPU and of empty workloads, and the validation
+leg's byte comparison (clean runs pass, planted mistakes are caught; the
+reference's tests/test_state_benchmark.py:34-76) are checked without one.
 """
 
 from __future__ import annotations
@@ -88,3 +90,128 @@ def test_ceiling_helpers_refuse_bad_arguments_before_any_device_work():
     assert lib.sr_stream_ceiling_p(n, 2, 4, 2, 2, 1, ms) == 1
     assert lib.sr_stream_ceiling_p(0, 4, 4, 2, 2, 1, ms) == 1
     assert bench.PLACEMENT_GAPS[0] == 0 and all(g % 256 == 0 and g <= 16 << 20 for g in bench.PLACEMENT_GAPS)
+
+
+@pytest.mark.parametrize("value,ok", [("1", True), ("1024", True), ("0", False), ("-1", False)])
+def test_positive_int(value, ok):
+    """benchmarks/bench_sgdm.py's argument types (tests/test_benchmark_helpers.py:14-31)."""
+    import argparse
+
+    if ok:
+        assert bench.positive_int(value) == int(value)
+    else:
+        with pytest.raises(argparse.ArgumentTypeError, match="positive"):
+            bench.positive_int(value)
+    assert bench.nonnegative_int("0") == 0
+    with pytest.raises(argparse.ArgumentTypeError, match="nonnegative"):
+        bench.nonnegative_int("-1")
+
+
+@pytest.mark.parametrize("option", ["--steps=0", "--warmup=-1", "--gpus=0", "--cpu-seconds=0", "--cpu-seconds=inf"])
+def test_nonpositive_workloads_are_refused(option):
+    """tests/test_state_benchmark.py:138-141: zero sizes and counts are refused before anything runs."""
+    result = subprocess.run([sys.executable, str(ROOT / "bench.py"), option], capture_output=True, text=True,
+                            timeout=300)
+    assert result.returncode == 2 and option.split("=")[0] in result.stderr
+
+
+@pytest.mark.parametrize(
+    "optimizer,p_dtype,state_dtype,expected",
+    [("sgdm", torch.float32, torch.bfloat16, 16), ("sgdm", torch.float32, torch.float32, 20),
+     ("adamw", torch.float32, torch.bfloat16, 20), ("adamw", torch.float32, torch.float32, 28),
+     ("sgdm", torch.bfloat16, torch.bfloat16, 10), ("sgdm", torch.bfloat16, torch.float32, 14),
+     ("adamw", torch.float32, torch.float8_e4m3fn, 16)],
+)
+def test_bytes_per_element_of_every_state_policy(optimizer, p_dtype, state_dtype, expected):
+    """tests/test_state_benchmark.py:125-135 and tests/test_benchmark_helpers.py:9-11."""
+    count = 2 if optimizer == "adamw" else 1
+    spec = {"optimizer": optimizer, "p_dtype": p_dtype, "g_dtype": p_dtype,
+            "formats": ((state_dtype, "stochastic"),) * count}
+    assert bench.bytes_per_element(spec) == expected
+
+
+# -- the validation leg ---------------------------------------------------------
+# validate() replays sampled chunks with the C oracle.  Here the "device" bytes
+# come from the torch restatement of the reference (oracle/sr_oracle.py), an
+# independent formulation, so a clean run checks the two against each other
+# and the planted mistakes check that the comparison sees them.
+
+SGDM_POLICIES = {
+    "bf16_sr": (torch.bfloat16, "stochastic"),
+    "fp16_sr": (torch.float16, "stochastic"),
+    "fp8e4_nr": (torch.float8_e4m3fn, "nearest"),
+    "fp8e4_sr": (torch.float8_e4m3fn, "stochastic"),
+    "fp8e5_nr": (torch.float8_e5m2, "nearest"),
+    "fp8e5_sr": (torch.float8_e5m2, "stochastic"),
+}
+FP8_POLICIES = ["fp8e4_nr", "fp8e4_sr", "fp8e5_nr", "fp8e5_sr"]
+
+
+def _sgdm_case(policy, steps=3):
+    from oracle import sr_oracle
+
+    spec = {"optimizer": "sgdm", "formats": (SGDM_POLICIES[policy],), "seed": 11,
+            "hparams": {"lr": 0.1, "momentum": 0.9}}
+    gen = torch.Generator().manual_seed(4)
+    samples, finals = [], []
+    for index, start, length in ((0, 0, 4099), (3, 8192 + 5, 1001)):
+        p0 = torch.randn(length, generator=gen)
+        g = torch.randn(length, generator=gen) * 0.05
+        samples.append((index, start, length, [p0, g]))
+        p, u = p0.clone(), torch.zeros(length, dtype=SGDM_POLICIES[policy][0])
+        for t in range(1, steps + 1):
+            key = sr_oracle.update_key(spec["seed"], t, index)
+            p, u = sr_oracle.sgdm_step(p, g, u, lr=0.1, momentum_factor=0.9,
+                                       formats=(sr_oracle.Fmt(*SGDM_POLICIES[policy]),), seed=key, offset=start)
+        finals.append([p, u])
+    return spec, samples, finals
+
+
+@pytest.mark.parametrize("policy", list(SGDM_POLICIES))
+def test_validation_accepts_the_reference_update(policy):
+    spec, samples, finals = _sgdm_case(policy)
+    result = bench.validate(spec, samples, finals, steps=3)
+    assert result["mismatches"] == 0
+    assert result["elements_checked"] == 2 * (4099 + 1001) and result["chunks"] == 2
+
+
+@pytest.mark.parametrize("policy", FP8_POLICIES)
+def test_validation_rejects_wrong_storage_with_correct_recurrence(policy):
+    """tests/test_state_benchmark.py:48-61: one storage step off is caught."""
+    spec, samples, finals = _sgdm_case(policy)
+    u = finals[0][1]
+    finals[0][1] = (u.float() + torch.finfo(u.dtype).eps).to(u.dtype)
+    assert bench.validate(spec, samples, finals, steps=3)["mismatches"] > 0
+
+
+@pytest.mark.parametrize("policy", FP8_POLICIES)
+def test_validation_rejects_wrong_fp32_recurrence(policy):
+    """tests/test_state_benchmark.py:63-76."""
+    spec, samples, finals = _sgdm_case(policy)
+    u = finals[1][1]
+    finals[1][1] = (u.float() + 0.0625).to(u.dtype)
+    assert bench.validate(spec, samples, finals, steps=3)["mismatches"] > 0
+
+
+def test_validation_counts_single_changes_and_step_counts():
+    spec, samples, finals = _sgdm_case("bf16_sr")
+    p = finals[1][0]
+    p.view(torch.int32)[:7] += 1  # seven parameters one ulp off
+    assert bench.validate(spec, samples, finals, steps=3)["mismatches"] == 7
+    spec, samples, finals = _sgdm_case("bf16_sr", steps=2)
+    assert bench.validate(spec, samples, finals, steps=3)["mismatches"] > 0
+
+
+@pytest.mark.parametrize("dtype,rule", [(torch.bfloat16, "stochastic"), (torch.float8_e4m3fn, "stochastic"),
+                                        (torch.float16, "nearest")])
+def test_validation_of_casts(dtype, rule):
+    from oracle import sr_oracle
+
+    spec = {"optimizer": "cast", "formats": ((dtype, rule),), "seed": 7}
+    x = torch.randn(3001, generator=torch.Generator().manual_seed(2)) * 50
+    samples = [(0, 5, 3001, [x])]
+    finals = [[sr_oracle.cast(x, dtype=dtype, rounding=rule, seed=7, offset=5)]]
+    assert bench.validate(spec, samples, finals, steps=1)["mismatches"] == 0
+    finals = [[sr_oracle.cast(x, dtype=dtype, rounding=rule, seed=7, offset=6)]]
+    if rule == "stochastic":  # another counter base draws other bits
+        assert bench.validate(spec, samples, finals, steps=1)["mismatches"] > 0
