@@ -2,7 +2,10 @@
 
 Gradients come from autograd and ``zero_grad(set_to_none=True)`` hands the
 optimizer new gradient tensors every step, as in real training; the
-steady-state path must notice every address change.  With FP32 states the
+steady-state path must notice every address change.  Gradient accumulation
+with ``zero_grad(set_to_none=False)`` keeps the tensors instead, and frozen
+layers bring gradients late or never; those runs are replayed through the C
+oracle byte for byte.  With FP32 states the
 fused AdamW follows ``torch.optim.AdamW`` (the eager reference's FP32
 recurrence differs from torch's only in operation order,
 tests/test_reference_optimizers.py:8-40 of the reference); with BF16 SR
@@ -91,3 +94,66 @@ def test_sr_states_train_like_fp32_states(cuda, kind, monkeypatch):
     # validates the layout) take the validating path; later steps patch or
     # reuse the gradient columns.
     assert validations_sr == 2
+
+
+@pytest.mark.parametrize("kind", ["adamw", "sgd"])
+def test_accumulated_and_frozen_gradients_against_the_oracle(cuda, kind):
+    """Gradient accumulation with ``zero_grad(set_to_none=False)`` (gradients keep their tensors),
+    a layer frozen for the first steps and a bias frozen throughout.
+
+    Each step is replayed through the C oracle from the gradients it saw:
+    grad-less parameters keep their index and their own AdamW step count
+    (optim/_state.py:154-200), so every byte must match.
+    """
+    import sr_states
+    from oracle import c_oracle, sr_oracle
+
+    x, y, model = _problem(cuda)
+    params = list(model.parameters())
+    first_layer, last_bias = params[:2], params[-1]
+    for p in first_layer:
+        p.requires_grad_(False)
+    last_bias.requires_grad_(False)
+    initial = [p.detach().cpu().clone() for p in params]
+    if kind == "adamw":
+        formats = ((torch.bfloat16, "stochastic"),) * 2
+        optimizer = sr_states.AdamWHip(params, lr=3e-3, weight_decay=0.01, seed=31)
+    else:
+        formats = ((torch.float16, "stochastic"),)
+        optimizer = sr_states.SGDMHip(params, lr=0.05, momentum=0.9, state_dtype=torch.float16, seed=31)
+    seen = []
+    for step in range(1, 7):
+        if step == 4:
+            for p in first_layer:
+                p.requires_grad_(True)
+        optimizer.zero_grad(set_to_none=False)
+        for rows in (slice(0, 1024), slice(1024, 2048)):  # two accumulated micro-batches
+            torch.nn.functional.mse_loss(model(x[rows]), y[rows]).backward()
+        seen.append([None if p.grad is None else p.grad.detach().cpu().clone() for p in params])
+        optimizer.step()
+    assert seen[0][0] is None and seen[3][0] is not None and all(s[-1] is None for s in seen)
+
+    want = [p.clone() for p in initial]
+    states = [[torch.zeros_like(p, dtype=f[0]) for f in formats] for p in want]
+    counts = [0] * len(want)
+    for rng_step, grads in enumerate(seen, start=1):
+        for index, (p, g, s) in enumerate(zip(want, grads, states)):
+            if g is None:
+                continue
+            counts[index] += 1
+            key = sr_oracle.update_key(31, rng_step, index)
+            if kind == "adamw":
+                c_oracle.adamw_step_(p, g, *s, lr=3e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01,
+                                     step=counts[index], formats=formats, seed=key)
+            else:
+                c_oracle.sgdm_step_(p, g, *s, lr=0.05, momentum_factor=0.9, formats=formats, seed=key)
+    for index, (p, w, s) in enumerate(zip(params, want, states)):
+        assert torch.equal(p.detach().cpu().view(torch.int32), w.view(torch.int32)), index
+        if counts[index] == 0:
+            assert p not in optimizer.state or not optimizer.state[p]
+            continue
+        for name, expected in zip(optimizer._state_names, s):
+            got = optimizer.state[p][name].cpu()
+            assert torch.equal(got.view(torch.int16), expected.view(torch.int16)), (index, name)
+        if kind == "adamw":
+            assert optimizer.state[p]["step"] == counts[index]
