@@ -33,6 +33,12 @@ same process after the workload's tensors are freed, also over
 back-to-back launches: what the memory system gives this access pattern at
 this footprint.  ``frac`` there is the fused kernel's rate over it.
 
+``torch_fused``: torch's own ``torch.optim.AdamW`` / ``SGD`` with
+``fused=True`` and FP32 states, timed the same way on the same parameters
+and gradients after the fused SR steps (the vendor baseline the reference's
+step benchmark reports its speedup against); ``speedup`` is its time per
+step over the fused SR step's.
+
 cpu_baseline: the reference's eager CPU path (restated in oracle/sr_oracle.py
 with the same torch operations) timed on this host on a bounded sample of
 the same workload.  ``validation``, in the same leg: sampled chunks of the
@@ -119,6 +125,23 @@ WORKLOADS = {
         formats=((torch.bfloat16, "stochastic"), (torch.bfloat16, "stochastic")),
         grad_std=1e-3,
         hparams=dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
+        seed=7,
+    ),
+    # Llama 3.2 1B shapes, the reference benchmark's other model
+    # (benchmarks/bench_optimizer_steps.py:54-69): 146 tensors, 1,235,814,400
+    # elements, FP32 parameters and gradients, BF16-SR moments, with that
+    # benchmark's hyperparameters (bench_optimizer_steps.py:200-203).
+    "llama32_1b": dict(
+        optimizer="adamw",
+        shapes=[(128256, 2048)]
+        + [(2048,), (2048, 2048), (512, 2048), (512, 2048), (2048, 2048), (2048,),
+           (8192, 2048), (8192, 2048), (2048, 8192)] * 16
+        + [(2048,)],
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=((torch.bfloat16, "stochastic"), (torch.bfloat16, "stochastic")),
+        grad_std=1e-3,
+        hparams=dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2),
         seed=7,
     ),
     # Config 4: E4M3-SR first moment, BF16-SR second moment over the 1.5 G
@@ -451,6 +474,53 @@ def validate(spec, samples, finals, steps):
     }
 
 
+def torch_fused_baseline(spec, work, steps, warmup):
+    """torch's own fused optimizer with FP32 states on the workload's tensors, or None.
+
+    The reference's step benchmark times ``torch.optim.AdamW`` / ``SGD`` with
+    ``fused=True`` beside its own optimizers and reports the speedup
+    (benchmarks/bench_optimizer_steps.py:247-251, 440-449).  Here the same
+    parameters and gradients (FP32 only: torch's fused kernels take
+    gradients of the parameters' dtype) are stepped by torch's kernels after
+    the fused SR steps are timed and read back; the time per step comes from
+    two events around back-to-back steps, as for the product.
+    """
+    if spec["optimizer"] not in ("adamw", "sgdm") or spec["p_dtype"] != spec["g_dtype"]:
+        return None
+    params = []
+    for p in work.tensors:
+        q = torch.nn.Parameter(p.detach())  # shares p's memory
+        q.grad = p.grad
+        params.append(q)
+    hp = spec["hparams"]
+    if spec["optimizer"] == "adamw":
+        opt = torch.optim.AdamW(params, fused=True, **hp)
+        name, states = "torch.optim.AdamW(fused=True)", 2
+    else:
+        opt = torch.optim.SGD(params, lr=hp["lr"], momentum=hp["momentum"], fused=True)
+        name, states = "torch.optim.SGD(momentum, fused=True)", 1
+    try:
+        for _ in range(max(1, min(warmup, 25))):
+            opt.step()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            opt.step()
+        end.record()
+        torch.cuda.synchronize()
+    except RuntimeError as error:  # a torch build without the fused kernels
+        return {"optimizer": name, "error": str(error).splitlines()[0]}
+    ms = start.elapsed_time(end) / steps
+    size = lambda dt: torch.empty((), dtype=dt).element_size()  # noqa: E731
+    bpe = 2 * size(spec["p_dtype"]) + size(spec["g_dtype"]) + 2 * 4 * states
+    elements = sum(p.numel() for p in params)
+    del opt, params
+    return {"optimizer": name, "state_dtype": "float32", "ms_per_step": ms, "bytes_per_element": bpe,
+            "achieved_gbps": bpe * elements / (ms / 1e3) / 1e9,
+            "frac": bpe * elements / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS}
+
+
 def _median_step_seconds(opt, target_seconds: float, min_steps: int = 3) -> tuple[float, int]:
     opt.step()  # allocate states
     times = []
@@ -666,6 +736,8 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-ceiling", action="store_true",
                         help="skip the access-pattern ceiling measurement")
+    parser.add_argument("--no-torch-baseline", action="store_true",
+                        help="skip timing torch's fused optimizer with FP32 states on the same tensors")
     parser.add_argument("--cpu-seconds", type=positive_float, default=12.0)
     parser.add_argument("--state-format", default=None, metavar="DTYPE/RULE",
                         help="store every state of the workload in this format instead, e.g. "
@@ -815,9 +887,15 @@ def main():
         },
         "host_ms_submit": statistics.median(submit_ms),
         "host_ms_wall": statistics.median(wall_ms),
+        "torch_fused": None,
         "cpu_baseline": None,
         "validation": None,
     }
+    if not args.no_torch_baseline:
+        baseline = torch_fused_baseline(spec, work, args.steps, args.warmup)
+        if baseline is not None and "ms_per_step" in baseline:
+            baseline["speedup"] = baseline["ms_per_step"] / ms_per_step
+        result["torch_fused"] = baseline
     del work, step
     torch.cuda.empty_cache()
     if not args.no_ceiling:

@@ -41,6 +41,20 @@ def test_north_star_is_the_default_and_has_the_stated_size():
     assert spec.get("warmup", 25) == 25 and spec.get("steps", 100) == 100
 
 
+def test_llama_workload_has_the_reference_benchmark_shapes():
+    """benchmarks/bench_optimizer_steps.py:54-69: 146 tensors, 1.24 G elements."""
+    spec = bench.WORKLOADS["llama32_1b"]
+    assert len(spec["shapes"]) == 146
+    assert sum(math.prod(s) for s in spec["shapes"]) == 1_235_814_400
+    assert spec["hparams"] == dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2)
+
+
+def test_torch_baseline_applies_only_where_torch_fused_can_run():
+    """Casts, the copy and mixed-dtype gradients (C3's BF16 gradients on FP32 parameters) get none."""
+    for name in ("c1_cast_bf16", "cast_2e26_e4m3", "copy_calibration", "c3_gpt2"):
+        assert bench.torch_fused_baseline(bench.WORKLOADS[name], work=None, steps=1, warmup=0) is None
+
+
 def test_short_launches_warm_up_for_the_clock_ramp():
     """Each cast or sub-millisecond workload's default warmup spans at least ~0.3 s of GPU work."""
     rough_ms = {"c1_cast_bf16": 0.0165, "c2_single_2e26": 0.208, "c3_gpt2": 0.353, "cast_2e26_bf16": 0.061}
