@@ -34,7 +34,7 @@ back-to-back launches: what the memory system gives this access pattern at
 this footprint.  ``frac`` there is the fused kernel's rate over it.
 
 ``torch_fused``: torch's own ``torch.optim.AdamW`` / ``SGD`` with
-``fused=True`` and FP32 states, timed the same way on the same parameters
+``fused=True`` (states in the parameters' dtype), timed the same way on the same parameters
 and gradients after the fused SR steps (the vendor baseline the reference's
 step benchmark reports its speedup against); ``speedup`` is its time per
 step over the fused SR step's.
@@ -475,7 +475,7 @@ def validate(spec, samples, finals, steps):
 
 
 def torch_fused_baseline(spec, work, steps, warmup):
-    """torch's own fused optimizer with FP32 states on the workload's tensors, or None.
+    """torch's own fused optimizer on the workload's tensors, or None.
 
     The reference's step benchmark times ``torch.optim.AdamW`` / ``SGD`` with
     ``fused=True`` beside its own optimizers and reports the speedup
@@ -483,7 +483,8 @@ def torch_fused_baseline(spec, work, steps, warmup):
     parameters and gradients (FP32 only: torch's fused kernels take
     gradients of the parameters' dtype) are stepped by torch's kernels after
     the fused SR steps are timed and read back; the time per step comes from
-    two events around back-to-back steps, as for the product.
+    two events around back-to-back steps, as for the product.  torch keeps
+    its states in the parameters' dtype (FP32 for FP32 parameters).
     """
     if spec["optimizer"] not in ("adamw", "sgdm") or spec["p_dtype"] != spec["g_dtype"]:
         return None
@@ -513,10 +514,11 @@ def torch_fused_baseline(spec, work, steps, warmup):
         return {"optimizer": name, "error": str(error).splitlines()[0]}
     ms = start.elapsed_time(end) / steps
     size = lambda dt: torch.empty((), dtype=dt).element_size()  # noqa: E731
-    bpe = 2 * size(spec["p_dtype"]) + size(spec["g_dtype"]) + 2 * 4 * states
+    bpe = 2 * size(spec["p_dtype"]) + size(spec["g_dtype"]) + 2 * size(spec["p_dtype"]) * states
     elements = sum(p.numel() for p in params)
     del opt, params
-    return {"optimizer": name, "state_dtype": "float32", "ms_per_step": ms, "bytes_per_element": bpe,
+    return {"optimizer": name, "state_dtype": str(spec["p_dtype"]).replace("torch.", ""),
+            "ms_per_step": ms, "bytes_per_element": bpe,
             "achieved_gbps": bpe * elements / (ms / 1e3) / 1e9,
             "frac": bpe * elements / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS}
 
