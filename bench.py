@@ -37,7 +37,9 @@ this footprint.  ``frac`` there is the fused kernel's rate over it.
 ``fused=True`` (states in the parameters' dtype), timed the same way on the same parameters
 and gradients after the fused SR steps (the vendor baseline the reference's
 step benchmark reports its speedup against); ``speedup`` is its time per
-step over the fused SR step's.
+step over the fused SR step's.  For casts, ``torch_cast`` times torch's own
+conversion (``Tensor.copy_`` into the output dtype, round to nearest) on the
+same buffers.
 
 cpu_baseline: the reference's eager CPU path (restated in oracle/sr_oracle.py
 with the same torch operations) timed on this host on a bounded sample of
@@ -523,6 +525,45 @@ def torch_fused_baseline(spec, work, steps, warmup):
             "frac": bpe * elements / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS}
 
 
+def torch_cast_baseline(spec, work, steps, warmup):
+    """torch's own conversion (``Tensor.copy_`` into the output dtype, round to nearest) on the
+    cast workload's rotating buffer pairs, timed like the product's casts; None for other workloads.
+
+    The reference's cast benchmark times ``x.to(torch.bfloat16)`` beside its
+    own casts (benchmarks/bench_sr_cast.py:38-46); ``copy_`` into the
+    preallocated outputs is the same conversion kernel without the
+    allocation.
+    """
+    if spec["optimizer"] != "cast":
+        return None
+    inputs, outputs = work.casts
+    turn = [0]
+
+    def convert():
+        k = turn[0] = (turn[0] + 1) % len(inputs)
+        outputs[k].copy_(inputs[k])
+
+    op = "Tensor.copy_ to the output dtype (round to nearest)"
+    try:
+        for _ in range(warmup):
+            convert()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            convert()
+        end.record()
+        torch.cuda.synchronize()
+    except RuntimeError as error:  # a torch build without this conversion on the device
+        return {"op": op, "error": str(error).splitlines()[0]}
+    ms = start.elapsed_time(end) / steps
+    bpe = bytes_per_element(spec)
+    elements = inputs[0].numel()
+    return {"op": op, "ms_per_step": ms,
+            "bytes_per_element": bpe, "achieved_gbps": bpe * elements / (ms / 1e3) / 1e9,
+            "frac": bpe * elements / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS}
+
+
 def _median_step_seconds(opt, target_seconds: float, min_steps: int = 3) -> tuple[float, int]:
     opt.step()  # allocate states
     times = []
@@ -890,6 +931,7 @@ def main():
         "host_ms_submit": statistics.median(submit_ms),
         "host_ms_wall": statistics.median(wall_ms),
         "torch_fused": None,
+        "torch_cast": None,
         "cpu_baseline": None,
         "validation": None,
     }
@@ -898,6 +940,10 @@ def main():
         if baseline is not None and "ms_per_step" in baseline:
             baseline["speedup"] = baseline["ms_per_step"] / ms_per_step
         result["torch_fused"] = baseline
+        cast_baseline = torch_cast_baseline(spec, work, args.steps, args.warmup)
+        if cast_baseline is not None and "ms_per_step" in cast_baseline:
+            cast_baseline["speedup"] = cast_baseline["ms_per_step"] / ms_per_step
+        result["torch_cast"] = cast_baseline
     del work, step
     torch.cuda.empty_cache()
     if not args.no_ceiling:

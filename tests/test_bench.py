@@ -53,6 +53,8 @@ def test_torch_baseline_applies_only_where_torch_fused_can_run():
     """Casts, the copy and mixed-dtype gradients (C3's BF16 gradients on FP32 parameters) get none."""
     for name in ("c1_cast_bf16", "cast_2e26_e4m3", "copy_calibration", "c3_gpt2"):
         assert bench.torch_fused_baseline(bench.WORKLOADS[name], work=None, steps=1, warmup=0) is None
+    for name in ("north_star", "c5_sgdm_fp16", "copy_calibration"):
+        assert bench.torch_cast_baseline(bench.WORKLOADS[name], work=None, steps=1, warmup=0) is None
 
 
 def test_short_launches_warm_up_for_the_clock_ramp():
