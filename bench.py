@@ -48,6 +48,10 @@ timed workload's tensors, read before the first step and after the last,
 replayed through every step (warmup and both timed passes) by the C oracle
 and compared byte for byte; the run fails if any byte differs.
 
+``--workload cast_sizes`` times the reference cast benchmark's size sweep
+(2^10 to 2^24): this backend's stochastic and nearest BF16 casts and torch's
+conversion, per size.
+
 ``--workload bandwidth_matrix`` instead times trivial-math kernels that move
 subsets and rearrangements of the north star's streams at its footprint
 (tests/native/bandwidth_matrix.hip) and prints their rates.
@@ -248,6 +252,21 @@ WORKLOADS = {
         seed=0,
         steps=10,
         warmup=3,
+    ),
+    # The reference cast benchmark's size sweep (benchmarks/bench_sr_cast.py:
+    # 25-27: 2^10 to 2^24 in steps of 4x) of FP32 -> BF16: this backend's
+    # stochastic and nearest casts beside torch's conversion, per size.
+    "cast_sizes": dict(
+        optimizer="cast_sweep",
+        shapes=[(1 << k,) for k in range(10, 25, 2)],
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=((torch.bfloat16, "stochastic"),),
+        grad_std=1.0,
+        hparams={},
+        seed=7,
+        steps=2000,
+        warmup=5000,
     ),
     # Config 5: gradients with 5% exact zeros, 1% of magnitude below 2^-14
     # (FP16 subnormal range) and the rest N(0, 1e-2).
@@ -564,6 +583,49 @@ def torch_cast_baseline(spec, work, steps, warmup):
             "frac": bpe * elements / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS}
 
 
+def cast_sizes(spec, steps, warmup):
+    """Per-size time of the HIP stochastic and nearest BF16 casts and of torch's conversion.
+
+    Each size uses eight rotating input/output pairs (at least 512 MB of
+    traffic between reuses of a buffer for the larger sizes) and is timed
+    over back-to-back calls between two events, after ``warmup`` calls.
+    """
+    from sr_states import _lib
+    from sr_states.hip.cast import native_cast
+
+    device = torch.device("cuda", 0)
+    gen = torch.Generator(device=device).manual_seed(spec["seed"])
+    rows = []
+    for (n,) in spec["shapes"]:
+        inputs = [torch.empty(n, device=device).normal_(generator=gen) for _ in range(8)]
+        outputs = [torch.empty(n, device=device, dtype=torch.bfloat16) for _ in range(8)]
+        methods = {
+            "hip_sr": lambda k: native_cast(inputs[k], dtype=torch.bfloat16, rule=_lib.RULE_CODES["stochastic"],
+                                            seed=spec["seed"], out=outputs[k]),
+            "hip_rn": lambda k: native_cast(inputs[k], dtype=torch.bfloat16, rule=_lib.RULE_CODES["nearest"],
+                                            out=outputs[k]),
+            "torch_rn": lambda k: outputs[k].copy_(inputs[k]),
+        }
+        row = {"elements": n}
+        for name, call in methods.items():
+            for i in range(warmup):
+                call(i % 8)
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record()
+            for i in range(steps):
+                call(i % 8)
+            end.record()
+            torch.cuda.synchronize()
+            us = start.elapsed_time(end) / steps * 1e3
+            row[f"{name}_us"] = us
+            row[f"{name}_gbps"] = 6 * n / (us / 1e6) / 1e9
+        row["hip_sr_speedup_vs_torch_rn"] = row["torch_rn_us"] / row["hip_sr_us"]
+        rows.append(row)
+        del inputs, outputs
+    return rows
+
+
 def _median_step_seconds(opt, target_seconds: float, min_steps: int = 3) -> tuple[float, int]:
     opt.step()  # allocate states
     times = []
@@ -826,6 +888,15 @@ def main():
             "data": "constant fill, XOR folds", "elements": n,
             "note": "steps = launches per variant per round, warmup = interleaved rounds",
             "peak": HBM_PEAK_GBPS, "matrix": rows, "placements": placements}), flush=True)
+        return
+    if spec["optimizer"] == "cast_sweep":
+        rows = cast_sizes(spec, args.steps, args.warmup)
+        print(json.dumps({
+            "metric": "FP32 -> BF16 cast time per call by size, 1 MI355X", "value": rows[-1]["hip_sr_gbps"],
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded normal draws on the GPU)",
+            "note": "value = the stochastic cast at the largest size; rows hold every size and method",
+            "peak": HBM_PEAK_GBPS, "sizes": rows}), flush=True)
         return
     work = build(spec, device)
     step = work.step

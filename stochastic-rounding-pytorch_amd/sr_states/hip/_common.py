@@ -23,7 +23,8 @@ def _device_arch(device: torch.device) -> str:
 
 def validate_device(device: torch.device) -> None:
     """Reject tensors the gfx950 library cannot run on, before any launch."""
-    device = torch.device(device)
+    if not isinstance(device, torch.device):
+        device = torch.device(device)
     if device.type != "cuda":
         raise ValueError("fused state updates require GPU tensors")
     arch = _device_arch(device).split(":")[0]

@@ -97,7 +97,7 @@ def hip_adamw_step_(
         return
     (m_code, m_rule), (v_code, v_rule) = (native_codes(f.dtype, f.rounding) for f in resolved)
     hparams = adamw_hparams(lr, beta1, beta2, eps, weight_decay, step)
-    with torch.cuda.device(parameter.device):
+    with _lib.on_device(parameter.device):
         _lib.call(
             "sr_adamw_step",
             parameter.data_ptr(),
@@ -199,7 +199,7 @@ class AdamWHip(StateOptimizer):
 
         for launch in launches:
             dtypes = (*launch.codes, m_code, m_rule, v_code, v_rule)
-            with torch.cuda.device(launch.device):
+            with _lib.on_device(launch.device):
                 if isinstance(launch.steps, int):
                     scalars, row_scalars = hparams(launch.steps), None
                 else:

@@ -28,26 +28,28 @@ def native_cast(x, *, dtype, rule, seed=0, offset=0, threads=_DEFAULT_THREADS, o
     Returns a new tensor, or writes into ``out`` (contiguous, ``dtype``, x's
     shape and device, disjoint from x) when given.
     """
-    if x.device.type != "cuda":
-        raise ValueError(f"sr_states casts run on the GPU; got a {x.device.type} tensor")
-    validate_device(x.device)
+    device = x.device
+    if device.type != "cuda":
+        raise ValueError(f"sr_states casts run on the GPU; got a {device.type} tensor")
+    validate_device(device)
     if out is None:
-        output = torch.empty(x.shape, dtype=dtype, device=x.device)
+        output = torch.empty(x.shape, dtype=dtype, device=device)
     else:
         output = check_out(x, out, dtype)
-    if x.numel():
-        with torch.cuda.device(x.device):
+    n = x.numel()
+    if n:
+        with _lib.on_device(device):
             _lib.call(
                 "sr_cast",
                 x.data_ptr(),
                 output.data_ptr(),
-                x.numel(),
+                n,
                 _lib.DTYPE_CODES[dtype],
                 rule,
-                _lib.low32(seed),
-                _lib.low32(offset),
+                seed & 0xFFFFFFFF,
+                offset & 0xFFFFFFFF,
                 threads,
-                _lib.stream_handle(x.device),
+                _lib.stream_handle(device),
             )
     return output
 
@@ -63,7 +65,7 @@ def native_neighbors(x, dtype):
     lower = torch.empty(x.shape, dtype=dtype, device=x.device)
     upper = torch.empty(x.shape, dtype=dtype, device=x.device)
     if x.numel():
-        with torch.cuda.device(x.device):
+        with _lib.on_device(x.device):
             _lib.call(
                 "sr_neighbors",
                 x.data_ptr(),

@@ -75,7 +75,7 @@ def hip_sgdm_step_(
         return
     code, rule = native_codes(fmt.dtype, fmt.rounding)
     hparams = sgdm_hparams(lr, momentum_factor)
-    with torch.cuda.device(parameter.device):
+    with _lib.on_device(parameter.device):
         _lib.call(
             "sr_sgdm_step",
             parameter.data_ptr(),
@@ -154,7 +154,7 @@ class SGDMHip(StateOptimizer):
         seed, rng_word = _lib.low64(group["sr_seed"]), _lib.low64(rng_step)
         block_size = self._group_block_size(group)
         for launch in launches:
-            with torch.cuda.device(launch.device):
+            with _lib.on_device(launch.device):
                 _launch(
                     launch.tables,
                     (*launch.codes, code, rule),

@@ -199,6 +199,7 @@ def recorder(monkeypatch):
         monkeypatch.setattr(module, "_launch", record)
         monkeypatch.setattr(module, "validate_update_device", lambda *args: None)
     monkeypatch.setattr(torch.cuda, "device", lambda device: nullcontext())
+    monkeypatch.setattr(_lib, "on_device", lambda device: nullcontext())
     monkeypatch.setattr(_lib, "stream_handle", lambda device: 0)
     return launches
 
