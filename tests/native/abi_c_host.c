@@ -6,7 +6,8 @@
  * with the row table and tile map built here) on the default stream,
  * copies the results back and compares them byte for byte with the C
  * oracle (oracle/sr_oracle.c, test infrastructure linked in as the
- * checker).  Also checks that a bad argument comes back as SR_ERR_ARGUMENT
+ * checker).  sr_neighbors (BF16) is checked against the definition of the
+ * pair.  Also checks that a bad argument comes back as SR_ERR_ARGUMENT
  * with a message.  Prints one line per check and "abi_c_host ok" at the
  * end; exits nonzero on the first failure.
  *
@@ -93,6 +94,36 @@ int main(void) {
     if (check_hip(hipMemcpy(host, dy, (size_t)N * width, hipMemcpyDeviceToHost), "copy y")) return 1;
     oc_cast(x, want, N, dtype, rule, 7u, 3u);
     if (same(host, want, (size_t)N * width, what)) return 1;
+  }
+
+  /* Neighbours in BF16: each pair brackets x, carries x's sign, is two
+   * adjacent encodings or one, and is one exactly when x is a BF16 value. */
+  {
+    void* dz;
+    if (check_hip(hipMalloc(&dz, N * 2), "hipMalloc")) return 1;
+    if (check_rc(sr_neighbors(dx, dy, dz, N, SR_BF16, NULL), "sr_neighbors")) return 1;
+    uint16_t* lower = (uint16_t*)host;
+    uint16_t* upper = (uint16_t*)want;
+    if (check_hip(hipMemcpy(lower, dy, N * 2, hipMemcpyDeviceToHost), "copy lower") ||
+        check_hip(hipMemcpy(upper, dz, N * 2, hipMemcpyDeviceToHost), "copy upper"))
+      return 1;
+    hipFree(dz);
+    for (size_t i = 0; i < N; ++i) {
+      uint32_t xb, lb = (uint32_t)lower[i] << 16, ub = (uint32_t)upper[i] << 16;
+      float lo, hi;
+      memcpy(&xb, &x[i], 4);
+      memcpy(&lo, &lb, 4);
+      memcpy(&hi, &ub, 4);
+      const uint32_t sign = xb >> 31, lm = lower[i] & 0x7FFFu, um = upper[i] & 0x7FFFu;
+      const uint32_t step = sign ? lm - um : um - lm;
+      const int exact = (xb & 0xFFFFu) == 0;
+      if (!(lo <= x[i] && x[i] <= hi) || (lb >> 31) != sign || (ub >> 31) != sign || step > 1u ||
+          (step == 0u) != exact) {
+        printf("FAIL sr_neighbors bf16 at %zu: x %08x lower %04x upper %04x\n", i, xb, lower[i], upper[i]);
+        return 1;
+      }
+    }
+    printf("ok sr_neighbors bf16 (%d inputs)\n", N);
   }
 
   /* AdamW: FP32 p/g, BF16-SR moments from zero, step 3. */
