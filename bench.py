@@ -8,7 +8,7 @@ star; more for short launches, so that the warmup spans the few hundred
 milliseconds in which the GPU raises its clocks).
 
 Default workload ``north_star``: AdamW with stochastically rounded BF16
-moments over the 1.55 G-element multi-tensor set of BASELINE config 4's
+moments over the 1.55 G-element multi-tensor set of the mixed-FP8 config's
 shapes (7 blocks of 4x 4096x4096 + 3x 4096x11008, plus a 32000x4096
 embedding; FP32 parameters and gradients), lr=3e-4, betas=(0.9, 0.999),
 eps=1e-8, weight_decay=0.01, seed=7.  Inputs are synthetic (seeded normal

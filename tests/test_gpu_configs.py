@@ -1,4 +1,4 @@
-"""The BASELINE configurations at their full sizes on the GPU.
+"""The benchmark configurations (C1-C5 and the north star) at their full sizes on the GPU.
 
 Every element's update depends only on its own inputs, its flat index and the
 update key (sr_states/_hash.py:31-50; triton/adamw.py:102-157), so the C
