@@ -3,9 +3,10 @@
 Run ``python build.py`` from anywhere.  The AdamW instantiations are split
 into nine translation units (one per first-moment encoding) that compile in
 parallel; the shared library is linked in place next to the Python package,
-so it travels with the source tree.  The host-side group walk
-(csrc/group_walk.cpp, a CPython extension over torch's tensor type) is built
-alongside it as sr_states/_group_walk<EXT_SUFFIX>.
+so it travels with the source tree.  Two CPython extensions over torch's
+tensor type are built alongside it: the host-side group walk
+(csrc/group_walk.cpp -> sr_states/_group_walk<EXT_SUFFIX>) and the cast's
+native entry (csrc/cast_launch.cpp -> sr_states/_cast_launch<EXT_SUFFIX>).
 """
 
 from __future__ import annotations
@@ -28,6 +29,7 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
 WALK_OUTPUT = ROOT / "sr_states" / f"_group_walk{sysconfig.get_config_var('EXT_SUFFIX')}"
+CAST_LAUNCH_OUTPUT = ROOT / "sr_states" / f"_cast_launch{sysconfig.get_config_var('EXT_SUFFIX')}"
 
 # -ffp-contract=off: only the explicit fmaf() calls may fuse, matching the
 # eager CPU reference.  Division and sqrt stay IEEE correctly rounded.
@@ -57,8 +59,8 @@ def units() -> list[tuple[Path, list[str], Path]]:
     return jobs
 
 
-def walk_command(output: Path) -> list[str]:
-    """g++ line for the group-walk extension, against the running torch."""
+def walk_command(output: Path, source: Path = CSRC / "group_walk.cpp") -> list[str]:
+    """g++ line for a CPython extension against the running torch (the group walk by default)."""
     import torch.utils.cpp_extension as ext
 
     torch_lib = ext.library_paths()[0]
@@ -72,7 +74,7 @@ def walk_command(output: Path) -> list[str]:
         f"-D_GLIBCXX_USE_CXX11_ABI={int(__import__('torch')._C._GLIBCXX_USE_CXX11_ABI)}",
         f"-I{sysconfig.get_paths()['include']}",
         *(f"-I{path}" for path in ext.include_paths()),
-        str(CSRC / "group_walk.cpp"),
+        str(source),
         "-o",
         str(output),
         f"-L{torch_lib}",
@@ -105,6 +107,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     ]
     walk_tmp = WALK_OUTPUT.with_name(WALK_OUTPUT.name + ".tmp")
     commands.append(walk_command(walk_tmp))
+    launch_tmp = CAST_LAUNCH_OUTPUT.with_name(CAST_LAUNCH_OUTPUT.name + ".tmp")
+    commands.append(walk_command(launch_tmp, CSRC / "cast_launch.cpp"))
     workers = jobs or min(len(commands), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(workers) as pool:
         for cmd, _ in zip(commands, pool.map(_run, commands)):
@@ -116,6 +120,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     _run(link)
     os.replace(tmp, OUTPUT)
     os.replace(walk_tmp, WALK_OUTPUT)
+    os.replace(launch_tmp, CAST_LAUNCH_OUTPUT)
     return OUTPUT
 
 

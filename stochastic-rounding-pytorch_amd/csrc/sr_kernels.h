@@ -430,7 +430,7 @@ __global__ __launch_bounds__(kMaxBlock) void cast_kernel(const CastArgs a) {
 #pragma unroll
       for (int j = 0; j < G; ++j) x[j] = bits_f32(r[k][j]);
       uint32_t words[group_words(ENC)];
-      encode_group<ENC>(x, a.counter_base + static_cast<uint32_t>(i), words);
+      encode_group<ENC, true>(x, a.counter_base + static_cast<uint32_t>(i), words);
       store_group<ENC>(a.y, i, words);
     }
   } else {

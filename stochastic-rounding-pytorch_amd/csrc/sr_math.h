@@ -638,7 +638,9 @@ SR_HD void decode_group(const uint32_t (&words)[group_words(ENC)], float (&x)[kG
 
 // Encodes one group of FP32 values (bits b) with the random words
 // hash[k] (ignored by nearest encodings) into storage words of ENC.
-template <int ENC>
+// kFromMemory: the values were loaded as they are (the casts), so no FMA
+// result can fuse into a convert and the group needs no barrier against it.
+template <int ENC, bool kFromMemory = false>
 SR_HD void encode_group_with(const uint32_t (&b)[kGroup], const uint32_t (&hash)[kGroup],
                              uint32_t (&words)[group_words(ENC)]) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -669,8 +671,10 @@ SR_HD void encode_group_with(const uint32_t (&b)[kGroup], const uint32_t (&hash)
 #pragma unroll
     for (int k = 0; k < kGroup; ++k) {
       // The empty asm keeps an FMA producing b from fusing with the convert.
+      // Loaded values need none, and there it made the compiler wait for a
+      // group's load before issuing the next one.
       bits[k] = b[k];
-      __asm__("" : "+v"(bits[k]));
+      if constexpr (!kFromMemory) __asm__("" : "+v"(bits[k]));
       x[k] = __builtin_bit_cast(float, bits[k]);
     }
     const float sum = (x[0] + x[1]) + (x[2] + x[3]);
@@ -752,7 +756,7 @@ SR_HD void encode_group_with(const uint32_t (&b)[kGroup], const uint32_t (&hash)
 
 // Encodes one group with counters counter0 + k: the hash of each counter
 // for stochastic encodings (sr_states/_hash.py:31-50), nothing for nearest.
-template <int ENC>
+template <int ENC, bool kFromMemory = false>
 SR_HD void encode_group(const float (&x)[kGroup], uint32_t counter0, uint32_t (&words)[group_words(ENC)]) {
   uint32_t b[kGroup], hash[kGroup];
 #pragma unroll
@@ -760,7 +764,7 @@ SR_HD void encode_group(const float (&x)[kGroup], uint32_t counter0, uint32_t (&
     b[k] = f32_bits(x[k]);
     hash[k] = enc_stochastic(ENC) ? h32(counter0 + static_cast<uint32_t>(k)) : 0u;
   }
-  encode_group_with<ENC>(b, hash, words);
+  encode_group_with<ENC, kFromMemory>(b, hash, words);
 }
 
 // ---------------------------------------------------------------------------

@@ -195,6 +195,20 @@ def on_device(device: torch.device):
     return torch.cuda.device(device)
 
 
+_cast_launch = None
+
+
+def cast_launcher():
+    """The cast's native entry (sr_states/_cast_launch), bound to this library's sr_cast."""
+    global _cast_launch
+    if _cast_launch is None:
+        from . import _cast_launch as module
+
+        module.bind(ctypes.cast(library().sr_cast, ctypes.c_void_p).value)
+        _cast_launch = module
+    return _cast_launch
+
+
 def low64(value: int) -> int:
     return int(value) & 0xFFFFFFFFFFFFFFFF
 

@@ -32,25 +32,12 @@ def native_cast(x, *, dtype, rule, seed=0, offset=0, threads=_DEFAULT_THREADS, o
     if device.type != "cuda":
         raise ValueError(f"sr_states casts run on the GPU; got a {device.type} tensor")
     validate_device(device)
-    if out is None:
-        output = torch.empty(x.shape, dtype=dtype, device=device)
-    else:
-        output = check_out(x, out, dtype)
-    n = x.numel()
-    if n:
-        with _lib.on_device(device):
-            _lib.call(
-                "sr_cast",
-                x.data_ptr(),
-                output.data_ptr(),
-                n,
-                _lib.DTYPE_CODES[dtype],
-                rule,
-                seed & 0xFFFFFFFF,
-                offset & 0xFFFFFFFF,
-                threads,
-                _lib.stream_handle(device),
-            )
+    output = torch.empty(x.shape, dtype=dtype, device=device) if out is None else out
+    # The native entry checks `output` (dtype, shape, device, contiguity and
+    # no byte shared with x), then calls sr_cast with x's device current.
+    status = _lib.cast_launcher().cast(x, output, _lib.DTYPE_CODES[dtype], rule, seed, offset, threads,
+                                       _lib.stream_handle(device))
+    _lib.check("sr_cast", status)
     return output
 
 
@@ -76,21 +63,6 @@ def native_neighbors(x, dtype):
                 _lib.stream_handle(x.device),
             )
     return lower, upper
-
-
-def check_out(x, out, dtype):
-    """``out`` for a cast of ``x`` to ``dtype``: contiguous, same shape and device, disjoint.
-
-    Workgroups read x and write out concurrently, so any shared byte would
-    make the result depend on their timing.
-    """
-    if out.dtype != dtype or out.shape != x.shape or out.device != x.device or not out.is_contiguous():
-        raise ValueError("out must be a contiguous tensor of the requested dtype, shape and device")
-    if x.numel():
-        x_start, out_start = x.data_ptr(), out.data_ptr()
-        if x_start < out_start + out.nbytes and out_start < x_start + x.nbytes:
-            raise ValueError("out must not overlap the input")
-    return out
 
 
 def _launch_shape(block_size, num_warps):

@@ -71,10 +71,11 @@ __global__ void every_pair(uint32_t hi, unsigned long long* counters) {
 }
 
 // Elements of a group whose BF16 encoding differs from the integer forms'.
-template <int ENC>
+// kFromMemory selects the casts' form of the group encoder.
+template <int ENC, bool kFromMemory = false>
 __device__ unsigned long long group_mismatches(const uint32_t (&b)[sr::kGroup], const uint32_t (&r)[sr::kGroup]) {
   uint32_t words[sr::group_words(ENC)], got[sr::kGroup];
-  sr::encode_group_with<ENC>(b, r, words);
+  sr::encode_group_with<ENC, kFromMemory>(b, r, words);
   sr::unpack_group<ENC>(words, got);
   unsigned long long mismatches = 0;
   for (int k = 0; k < sr::kGroup; ++k) {
@@ -95,7 +96,8 @@ __device__ void randoms_of(uint32_t b, uint32_t (&r)[5]) {
 
 // Input x = base + thread at each position of a group beside hashed
 // companions: stochastic with each of the five random values of every
-// element, and nearest.  4 * 6 groups of 4 elements per thread.
+// element, and nearest in both the optimizers' and the casts' form.
+// 4 * 7 groups of 4 elements per thread.
 __global__ void every_input_group(uint32_t base, unsigned long long* counters) {
   const uint32_t x = base + blockIdx.x * blockDim.x + threadIdx.x;
   unsigned long long mismatches = 0;
@@ -111,8 +113,9 @@ __global__ void every_input_group(uint32_t base, unsigned long long* counters) {
     }
     const uint32_t zero[sr::kGroup] = {};
     mismatches += group_mismatches<sr::ENC_BF16_RN>(b, zero);
+    mismatches += group_mismatches<sr::ENC_BF16_RN, true>(b, zero);
   }
-  add(counters, mismatches, 4ull * 6 * sr::kGroup);
+  add(counters, mismatches, 4ull * 7 * sr::kGroup);
 }
 
 // every_pair at each position of a group, the other elements hashed inputs

@@ -166,21 +166,37 @@ def test_builtin_casts_never_run_on_the_cpu():
 
 
 def test_cast_output_must_not_overlap_the_input():
-    """native_cast(out=...) refuses an output sharing any byte with the input."""
-    from sr_states.hip.cast import check_out
+    """The cast's native entry refuses an output sharing any byte with the input.
+
+    Its output checks come before its device check, so CPU tensors show them
+    without a GPU: an acceptable output gets as far as the GPU requirement.
+    """
+    from sr_states import _lib
+
+    launcher = _lib.cast_launcher()
+    code = _lib.DTYPE_CODES
+
+    def error(x, out):
+        with pytest.raises(ValueError) as caught:
+            launcher.cast(x, out, code[out.dtype], _lib.SR_STOCHASTIC, 7, 0, 256, 0)
+        return str(caught.value)
 
     storage = torch.zeros(64)
     x = storage[:16]
-    check_out(x, torch.empty(16, dtype=torch.bfloat16), torch.bfloat16)  # disjoint
-    check_out(x, storage[16:24].view(torch.bfloat16), torch.bfloat16)  # adjacent
+    assert "GPU" in error(x, torch.empty(16, dtype=torch.bfloat16))  # disjoint
+    assert "GPU" in error(x, storage[16:24].view(torch.bfloat16))  # adjacent
     for out in (storage[:8].view(torch.bfloat16), storage[15:23].view(torch.bfloat16),
                 storage[10:14].view(torch.float8_e4m3fn)):
-        dtype = out.dtype
-        with pytest.raises(ValueError, match="overlap"):
-            check_out(x, out, dtype)
-    check_out(storage[:0], storage[:0].view(torch.bfloat16), torch.bfloat16)  # empty: nothing shared
-    with pytest.raises(ValueError, match="contiguous tensor"):
-        check_out(x, torch.empty(16, dtype=torch.float16), torch.bfloat16)
+        assert "overlap" in error(x, out)
+    assert "GPU" in error(storage[:0], storage[:0].view(torch.bfloat16))  # empty: nothing shared
+    with pytest.raises(ValueError, match="contiguous tensor of the requested dtype"):
+        launcher.cast(x, torch.empty(16, dtype=torch.float16), code[torch.bfloat16], 1, 7, 0, 256, 0)
+    with pytest.raises(ValueError, match="contiguous tensor of the requested dtype"):
+        launcher.cast(x, torch.empty(15, dtype=torch.bfloat16), code[torch.bfloat16], 1, 7, 0, 256, 0)
+    with pytest.raises(ValueError, match="contiguous tensor of the requested dtype"):
+        launcher.cast(x, torch.empty(32, dtype=torch.bfloat16)[::2], code[torch.bfloat16], 1, 7, 0, 256, 0)
+    with pytest.raises(TypeError, match="tensors"):
+        launcher.cast(x, [0.0] * 16, code[torch.bfloat16], 1, 7, 0, 256, 0)
 
 
 @pytest.mark.parametrize("arch", ["gfx950:sramecc+:xnack-", "gfx950", "gfx942:sramecc+:xnack-", "gfx90a", "gfx1100"])
