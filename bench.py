@@ -919,7 +919,7 @@ def main():
     total_ms = total_start.elapsed_time(total_end)
     ms_per_step = total_ms / args.steps
     # One launch per step, enqueued back to back on the launch stream with the
-    # host ahead of the GPU (host work per step: 9 us for the cast, 53 us for
+    # host ahead of the GPU (host work per step: 4 us for the cast, 55 us for
     # C3's 148 tensors), so the time per step is the kernel's average launch
     # duration.  No events sit between the steps: on an 18 us cast they would
     # add about 2 us each.
