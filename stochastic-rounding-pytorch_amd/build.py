@@ -5,8 +5,9 @@ into nine translation units (one per first-moment encoding) that compile in
 parallel; the shared library is linked in place next to the Python package,
 so it travels with the source tree.  Two CPython extensions over torch's
 tensor type are built alongside it: the host-side group walk
-(csrc/group_walk.cpp -> sr_states/_group_walk<EXT_SUFFIX>) and the cast's
-native entry (csrc/cast_launch.cpp -> sr_states/_cast_launch<EXT_SUFFIX>).
+(csrc/group_walk.cpp -> sr_states/_group_walk<EXT_SUFFIX>) and the native
+entries of the single-tensor launches (csrc/launch.cpp ->
+sr_states/_launch<EXT_SUFFIX>).
 """
 
 from __future__ import annotations
@@ -29,7 +30,7 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
 WALK_OUTPUT = ROOT / "sr_states" / f"_group_walk{sysconfig.get_config_var('EXT_SUFFIX')}"
-CAST_LAUNCH_OUTPUT = ROOT / "sr_states" / f"_cast_launch{sysconfig.get_config_var('EXT_SUFFIX')}"
+LAUNCH_OUTPUT = ROOT / "sr_states" / f"_launch{sysconfig.get_config_var('EXT_SUFFIX')}"
 
 # -ffp-contract=off: only the explicit fmaf() calls may fuse, matching the
 # eager CPU reference.  Division and sqrt stay IEEE correctly rounded.
@@ -107,8 +108,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     ]
     walk_tmp = WALK_OUTPUT.with_name(WALK_OUTPUT.name + ".tmp")
     commands.append(walk_command(walk_tmp))
-    launch_tmp = CAST_LAUNCH_OUTPUT.with_name(CAST_LAUNCH_OUTPUT.name + ".tmp")
-    commands.append(walk_command(launch_tmp, CSRC / "cast_launch.cpp"))
+    launch_tmp = LAUNCH_OUTPUT.with_name(LAUNCH_OUTPUT.name + ".tmp")
+    commands.append(walk_command(launch_tmp, CSRC / "launch.cpp"))
     workers = jobs or min(len(commands), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(workers) as pool:
         for cmd, _ in zip(commands, pool.map(_run, commands)):
@@ -120,7 +121,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     _run(link)
     os.replace(tmp, OUTPUT)
     os.replace(walk_tmp, WALK_OUTPUT)
-    os.replace(launch_tmp, CAST_LAUNCH_OUTPUT)
+    os.replace(launch_tmp, LAUNCH_OUTPUT)
     return OUTPUT
 
 

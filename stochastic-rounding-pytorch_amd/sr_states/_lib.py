@@ -195,18 +195,20 @@ def on_device(device: torch.device):
     return torch.cuda.device(device)
 
 
-_cast_launch = None
+_launcher = None
 
 
-def cast_launcher():
-    """The cast's native entry (sr_states/_cast_launch), bound to this library's sr_cast."""
-    global _cast_launch
-    if _cast_launch is None:
-        from . import _cast_launch as module
+def launcher():
+    """The native entries of the single-tensor launches (sr_states/_launch), bound to this library."""
+    global _launcher
+    if _launcher is None:
+        from . import _launch as module
 
-        module.bind(ctypes.cast(library().sr_cast, ctypes.c_void_p).value)
-        _cast_launch = module
-    return _cast_launch
+        lib = library()
+        module.bind(*(ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+                      for name in ("sr_cast", "sr_adamw_step", "sr_sgdm_step")))
+        _launcher = module
+    return _launcher
 
 
 def low64(value: int) -> int:

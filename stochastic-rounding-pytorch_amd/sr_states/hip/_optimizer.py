@@ -7,8 +7,9 @@ from bisect import bisect_left
 
 import torch
 
-from ..optim._dtensor import is_dtensor
-from ..rounding import validate_rounding
+from ..formats import StateFormat, resolve_formats
+from ..optim._dtensor import DTensor
+from ..rounding import native_codes, validate_rounding
 
 # Workgroup sizes (threads).  Results do not depend on the choice.
 BLOCK_SIZES = (128, 256, 512, 1024)
@@ -71,17 +72,48 @@ def validate_no_overlap(spans):
         raise ValueError("parameter, gradient, and state must not overlap optimizer writes")
 
 
-def validate_tensors(parameter, gradient, *states):
-    tensors = (parameter, gradient, *states)
-    if any(is_dtensor(t) for t in tensors):
-        raise TypeError(
-            "fused state updates take local tensors: pass each DTensor's to_local() and the "
-            "flat index of the shard's first element as offset"
-        )
-    if parameter.device.type != "cuda":
-        raise ValueError("fused state updates require GPU tensors")
-    validate_tensor_layout(tensors)
-    if parameter.numel():
-        validate_no_overlap(
-            (t.data_ptr(), t.data_ptr() + t.nbytes, role != 1) for role, t in enumerate(tensors)
-        )
+def reject_dtensors(*tensors):
+    """The functional updates take local tensors (the native entries check the rest)."""
+    if DTensor is not None:
+        for tensor in tensors:
+            if isinstance(tensor, DTensor):
+                raise TypeError(
+                    "fused state updates take local tensors: pass each DTensor's to_local() and the "
+                    "flat index of the shard's first element as offset"
+                )
+
+
+# Successful resolutions of the functional updates' formats.  Only built-in
+# rules have HIP implementations, and a registration can never replace one,
+# so a resolution that succeeded once holds for the life of the process.
+_NATIVE_CODES: dict = {}
+
+
+def resolve_native_codes(names, states, formats, rounding, block_size):
+    """Each state's (sr_dtype, sr_rule) for one functional update (triton/adamw.py:196-205).
+
+    ``formats`` None takes every state's own dtype with ``rounding``
+    (stochastic by default).  Raises as ``resolve_formats`` and
+    ``validate_options`` do, and when a state's dtype is not its format's.
+    """
+    dtypes = tuple(state.dtype for state in states)
+    key = (names, dtypes, formats, rounding, block_size)
+    try:
+        return _NATIVE_CODES[key]
+    except KeyError:
+        pass
+    except TypeError:  # unhashable formats (a dict): resolve every time
+        key = None
+    if formats is None:
+        rule = "stochastic" if rounding is None else rounding
+        resolved = resolve_formats(names, tuple(StateFormat(d, rule) for d in dtypes), backend="hip")
+    else:
+        resolved = resolve_formats(names, formats, rounding=rounding, backend="hip")
+    for dtype, fmt in zip(dtypes, resolved):
+        validate_options(fmt.rounding, block_size, fmt.dtype)
+        if dtype != fmt.dtype:
+            raise ValueError("state dtype does not match its state format")
+    codes = tuple(native_codes(fmt.dtype, fmt.rounding) for fmt in resolved)
+    if key is not None and len(_NATIVE_CODES) < 1024:
+        _NATIVE_CODES[key] = codes
+    return codes

@@ -13,13 +13,20 @@ import numpy as np
 import torch
 
 from .. import _lib
-from ..formats import StateFormat, resolve_formats
 from ..optim._state import StateOptimizer
-from ..optim.adamw import adamw_hparams, validate_adamw
+from ..optim.adamw import adamw_hparams, adamw_scalars, validate_adamw
 from ..rounding import native_codes
 from ._common import validate_device, validate_update_device
 from ._multi_tensor import prepare_group, upload
-from ._optimizer import DEFAULT_BLOCK_SIZE, nonnegative, validate_options, validate_tensors
+from ._optimizer import (
+    DEFAULT_BLOCK_SIZE,
+    nonnegative,
+    reject_dtensors,
+    resolve_native_codes,
+    validate_options,
+)
+
+_STATE_NAMES = ("exp_avg", "exp_avg_sq")
 
 
 def _launch(tables, dtypes, hparams, seed, rng_step, block_size, stream, row_scalars=None):
@@ -79,44 +86,25 @@ def hip_adamw_step_(
     ``seed`` is the update key and ``offset`` the flat index of the first
     element.
     """
-    if formats is None:
-        rule = "stochastic" if rounding is None else rounding
-        formats = (StateFormat(exp_avg.dtype, rule), StateFormat(exp_avg_sq.dtype, rule))
-        rounding = None
-    resolved = resolve_formats(("exp_avg", "exp_avg_sq"), formats, rounding=rounding, backend="hip")
-    for state, fmt in zip((exp_avg, exp_avg_sq), resolved):
-        validate_options(fmt.rounding, block_size, fmt.dtype)
-        if state.dtype != fmt.dtype:
-            raise ValueError("state dtype does not match its state format")
+    (m_code, m_rule), (v_code, v_rule) = resolve_native_codes(
+        _STATE_NAMES, (exp_avg, exp_avg_sq), formats, rounding, block_size
+    )
     _validate_hyperparameters(lr, (beta1, beta2), eps, weight_decay)
     if not isinstance(step, int) or isinstance(step, bool) or step < 1:
         raise ValueError("step must be a positive integer")
-    validate_tensors(parameter, gradient, exp_avg, exp_avg_sq)
-    validate_device(parameter.device)
-    if parameter.numel() == 0:
-        return
-    (m_code, m_rule), (v_code, v_rule) = (native_codes(f.dtype, f.rounding) for f in resolved)
-    hparams = adamw_hparams(lr, beta1, beta2, eps, weight_decay, step)
-    with _lib.on_device(parameter.device):
-        _lib.call(
-            "sr_adamw_step",
-            parameter.data_ptr(),
-            gradient.data_ptr(),
-            exp_avg.data_ptr(),
-            exp_avg_sq.data_ptr(),
-            parameter.numel(),
-            _lib.DTYPE_CODES[parameter.dtype],
-            _lib.DTYPE_CODES[gradient.dtype],
-            m_code,
-            m_rule,
-            v_code,
-            v_rule,
-            ctypes.byref(hparams),
-            _lib.low32(seed),
-            _lib.low32(offset),
-            block_size,
-            _lib.stream_handle(parameter.device),
-        )
+    reject_dtensors(parameter, gradient, exp_avg, exp_avg_sq)
+    device = parameter.device
+    if device.type != "cuda":
+        raise ValueError("fused state updates require GPU tensors")
+    validate_device(device)
+    # The native entry checks devices, shapes, layout, dtypes and overlap with
+    # the messages of sr_states/triton/_optimizer.py:24-60, then launches.
+    status = _lib.launcher().adamw_step(
+        parameter, gradient, exp_avg, exp_avg_sq, m_code, m_rule, v_code, v_rule,
+        adamw_scalars(lr, beta1, beta2, eps, weight_decay, step), _lib.low32(seed), _lib.low32(offset), block_size,
+        _lib.stream_handle(device),
+    )
+    _lib.check("sr_adamw_step", status)
 
 
 class AdamWHip(StateOptimizer):
@@ -127,7 +115,7 @@ class AdamWHip(StateOptimizer):
     threads; results do not depend on it.
     """
 
-    _state_names = ("exp_avg", "exp_avg_sq")
+    _state_names = _STATE_NAMES
     _uses_step = True
     _rounding_backend = "hip"
 

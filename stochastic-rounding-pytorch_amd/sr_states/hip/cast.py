@@ -35,8 +35,8 @@ def native_cast(x, *, dtype, rule, seed=0, offset=0, threads=_DEFAULT_THREADS, o
     output = torch.empty(x.shape, dtype=dtype, device=device) if out is None else out
     # The native entry checks `output` (dtype, shape, device, contiguity and
     # no byte shared with x), then calls sr_cast with x's device current.
-    status = _lib.cast_launcher().cast(x, output, _lib.DTYPE_CODES[dtype], rule, seed, offset, threads,
-                                       _lib.stream_handle(device))
+    status = _lib.launcher().cast(x, output, _lib.DTYPE_CODES[dtype], rule, _lib.low32(seed),
+                                  _lib.low32(offset), threads, _lib.stream_handle(device))
     _lib.check("sr_cast", status)
     return output
 

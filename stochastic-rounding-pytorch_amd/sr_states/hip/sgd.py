@@ -11,13 +11,20 @@ import ctypes
 import torch
 
 from .. import _lib
-from ..formats import StateFormat, resolve_formats
 from ..optim._state import StateOptimizer
-from ..optim.sgd import sgdm_hparams, validate_sgdm
+from ..optim.sgd import sgdm_hparams, sgdm_scalars, validate_sgdm
 from ..rounding import native_codes
 from ._common import validate_device, validate_update_device
 from ._multi_tensor import prepare_group
-from ._optimizer import DEFAULT_BLOCK_SIZE, nonnegative, validate_options, validate_tensors
+from ._optimizer import (
+    DEFAULT_BLOCK_SIZE,
+    nonnegative,
+    reject_dtensors,
+    resolve_native_codes,
+    validate_options,
+)
+
+_STATE_NAMES = ("momentum_buffer",)
 
 
 def _launch(tables, dtypes, hparams, seed, rng_step, block_size, stream):
@@ -58,40 +65,22 @@ def hip_sgdm_step_(
     any built-in storage format.  ``seed`` is the update key and ``offset``
     the flat index of the first element.
     """
-    if formats is None:
-        formats = (StateFormat(momentum.dtype, "stochastic" if rounding is None else rounding),)
-        rounding = None
-    resolved = resolve_formats(("momentum_buffer",), formats, rounding=rounding, backend="hip")
-    fmt = resolved[0]
-    validate_options(fmt.rounding, block_size, fmt.dtype)
-    if momentum.dtype != fmt.dtype:
-        raise ValueError("state dtype does not match its state format")
+    ((code, rule),) = resolve_native_codes(_STATE_NAMES, (momentum,), formats, rounding, block_size)
     nonnegative("learning rate", lr)
     if not 0 <= momentum_factor < 1:
         raise ValueError(f"invalid momentum value: {momentum_factor}")
-    validate_tensors(parameter, gradient, momentum)
-    validate_device(parameter.device)
-    if parameter.numel() == 0:
-        return
-    code, rule = native_codes(fmt.dtype, fmt.rounding)
-    hparams = sgdm_hparams(lr, momentum_factor)
-    with _lib.on_device(parameter.device):
-        _lib.call(
-            "sr_sgdm_step",
-            parameter.data_ptr(),
-            gradient.data_ptr(),
-            momentum.data_ptr(),
-            parameter.numel(),
-            _lib.DTYPE_CODES[parameter.dtype],
-            _lib.DTYPE_CODES[gradient.dtype],
-            code,
-            rule,
-            ctypes.byref(hparams),
-            _lib.low32(seed),
-            _lib.low32(offset),
-            block_size,
-            _lib.stream_handle(parameter.device),
-        )
+    reject_dtensors(parameter, gradient, momentum)
+    device = parameter.device
+    if device.type != "cuda":
+        raise ValueError("fused state updates require GPU tensors")
+    validate_device(device)
+    # The native entry checks devices, shapes, layout, dtypes and overlap with
+    # the messages of sr_states/triton/_optimizer.py:24-60, then launches.
+    status = _lib.launcher().sgdm_step(
+        parameter, gradient, momentum, code, rule, sgdm_scalars(lr, momentum_factor), _lib.low32(seed),
+        _lib.low32(offset), block_size, _lib.stream_handle(device),
+    )
+    _lib.check("sr_sgdm_step", status)
 
 
 class SGDMHip(StateOptimizer):
@@ -102,7 +91,7 @@ class SGDMHip(StateOptimizer):
     option, as in the reference.
     """
 
-    _state_names = ("momentum_buffer",)
+    _state_names = _STATE_NAMES
     _uses_step = False
     _rounding_backend = "hip"
 

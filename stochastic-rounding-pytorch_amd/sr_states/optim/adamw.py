@@ -17,26 +17,25 @@ def validate_adamw(group):
         raise ValueError(f"invalid beta values: {betas}")
 
 
-def adamw_hparams(lr, beta1, beta2, eps, weight_decay, step) -> _lib.AdamWHparams:
-    """Launch scalars for one bias-correction step.
+def adamw_scalars(lr, beta1, beta2, eps, weight_decay, step) -> tuple:
+    """Launch scalars for one bias-correction step, as Python doubles.
 
-    The eager reference evaluates each scalar in Python double precision and
-    rounds it to FP32 when it meets an FP32 tensor
-    (sr_states/reference/adamw.py:86-96); ctypes' c_float conversion performs
-    the same round-to-nearest.
+    In the order of sr_adamw_hparams' fields: beta1, beta2, 1 - beta1,
+    1 - beta2, -lr / (1 - beta1^step), sqrt(1 - beta2^step),
+    1 - lr * weight_decay, eps.  The eager reference evaluates each in Python
+    double precision and rounds it to FP32 when it meets an FP32 tensor
+    (sr_states/reference/adamw.py:86-96); the launches round each the same
+    way (ctypes' c_float conversion, or a C cast in the native entries).
     """
     bias_correction1 = 1.0 - beta1**step
     bias_correction2 = 1.0 - beta2**step
-    return _lib.AdamWHparams(
-        beta1=beta1,
-        beta2=beta2,
-        one_minus_beta1=1.0 - beta1,
-        one_minus_beta2=1.0 - beta2,
-        neg_step_size=-lr / bias_correction1,
-        correction2_sqrt=bias_correction2**0.5,
-        decay=1.0 - lr * weight_decay,
-        eps=eps,
-    )
+    return (beta1, beta2, 1.0 - beta1, 1.0 - beta2, -lr / bias_correction1, bias_correction2**0.5,
+            1.0 - lr * weight_decay, eps)
+
+
+def adamw_hparams(lr, beta1, beta2, eps, weight_decay, step) -> _lib.AdamWHparams:
+    """``adamw_scalars`` rounded to FP32 in the C ABI's sr_adamw_hparams."""
+    return _lib.AdamWHparams(*adamw_scalars(lr, beta1, beta2, eps, weight_decay, step))
 
 
 def __getattr__(name):

@@ -15,9 +15,14 @@ def validate_sgdm(group):
         raise ValueError(f"invalid momentum value: {group['momentum']}")
 
 
+def sgdm_scalars(lr, momentum) -> tuple:
+    """Scalars of ``u = u*momentum + g; p = p + (-lr)*u`` (reference/sgd.py:62-64), as doubles."""
+    return (momentum, -lr)
+
+
 def sgdm_hparams(lr, momentum) -> _lib.SgdmHparams:
-    """FP32 scalars of ``u = u*momentum + g; p = p + (-lr)*u`` (reference/sgd.py:62-64)."""
-    return _lib.SgdmHparams(momentum=momentum, neg_lr=-lr)
+    """``sgdm_scalars`` rounded to FP32 in the C ABI's sr_sgdm_hparams."""
+    return _lib.SgdmHparams(*sgdm_scalars(lr, momentum))
 
 
 def __getattr__(name):

@@ -213,3 +213,70 @@ def test_validation_and_disjoint_buffers(cuda, kind):
         with pytest.raises(ValueError, match="state dtype"):
             function(*tensors[:-1], tensors[-1].bfloat16(),
                      formats=(StateFormat(torch.float32), StateFormat(torch.float32)), **options)
+
+
+@pytest.mark.parametrize("kind", ["adamw", "sgdm"])
+def test_refused_updates_launch_nothing_and_keys_wrap_modulo_2_32(cuda, kind):
+    """The update entries' tensor checks (triton/_optimizer.py:24-60) refuse before any launch.
+
+    A written tensor sharing a byte with any other operand is refused, a
+    gradient only next to the parameter is not; a tensor on another device
+    and an FP16 parameter are refused; empty tensors launch nothing.  Keys
+    and offsets are taken modulo 2^32, as the ctypes path took them.
+    """
+    import sr_states
+
+    formats = [(torch.bfloat16, "stochastic")] * (2 if kind == "adamw" else 1)
+    function = sr_states.hip_adamw_step_ if kind == "adamw" else sr_states.hip_sgdm_step_
+    options = {**ADAMW} if kind == "adamw" else {**SGDM}
+    fmts = tuple(sr_states.StateFormat(d, r) for d, r in formats)
+    n = 257
+    host = _inputs(kind, n, torch.float32, torch.float32, formats)
+
+    def fresh():
+        return [t.to(cuda) for t in host]
+
+    def nbytes(t):
+        return t.numel() * t.element_size()
+
+    # Every (written, other) pair carved from one byte buffer, the other
+    # starting a few bytes before the written one ends.
+    for written in [0] + list(range(2, len(host))):
+        for other in range(len(host)):
+            if other == written:
+                continue
+            tensors = fresh()
+            start = (nbytes(host[written]) - 4) & ~3
+            shared = torch.zeros(start + nbytes(host[other]), dtype=torch.uint8, device=cuda)
+            for role, begin in ((written, 0), (other, start)):
+                tensors[role] = shared[begin:begin + nbytes(host[role])].view(host[role].dtype)
+                tensors[role].copy_(host[role])
+            before = [t.clone() for t in tensors]
+            with pytest.raises(ValueError, match="must not overlap optimizer writes"):
+                function(*tensors, seed=5, formats=fmts, **options)
+            assert all(torch.equal(a.view(torch.uint8), b.view(torch.uint8)) for a, b in zip(tensors, before))
+    # A gradient only adjacent to the parameter is accepted and gives the usual update.
+    buffer = torch.empty(2 * n, device=cuda)
+    adjacent = fresh()
+    buffer[:n].copy_(adjacent[0])
+    buffer[n:].copy_(adjacent[1])
+    adjacent[0], adjacent[1] = buffer[:n], buffer[n:]
+    separate = fresh()
+    function(*adjacent, seed=5, formats=fmts, **options)
+    function(*separate, seed=5, formats=fmts, **options)
+    for a, b in zip(adjacent, separate):
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+
+    tensors = fresh()
+    with pytest.raises(ValueError, match="same GPU device"):
+        function(*tensors[:-1], tensors[-1].cpu(), seed=5, formats=fmts, **options)
+    with pytest.raises(TypeError, match="FP32 or BF16"):
+        function(tensors[0].half(), *tensors[1:], seed=5, formats=fmts, **options)
+    empty = [t[:0] for t in tensors]
+    function(*empty, seed=5, formats=fmts, **options)
+
+    wrapped, plain = fresh(), fresh()
+    function(*wrapped, seed=5 + 3 * 2**32, offset=-2**32 + 11, formats=fmts, **options)
+    function(*plain, seed=5, offset=11, formats=fmts, **options)
+    for a, b in zip(wrapped, plain):
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))

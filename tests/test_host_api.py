@@ -173,7 +173,7 @@ def test_cast_output_must_not_overlap_the_input():
     """
     from sr_states import _lib
 
-    launcher = _lib.cast_launcher()
+    launcher = _lib.launcher()
     code = _lib.DTYPE_CODES
 
     def error(x, out):
@@ -197,6 +197,42 @@ def test_cast_output_must_not_overlap_the_input():
         launcher.cast(x, torch.empty(32, dtype=torch.bfloat16)[::2], code[torch.bfloat16], 1, 7, 0, 256, 0)
     with pytest.raises(TypeError, match="tensors"):
         launcher.cast(x, [0.0] * 16, code[torch.bfloat16], 1, 7, 0, 256, 0)
+
+
+def test_update_entries_check_their_tensors_before_the_device():
+    """The functional updates' native entries: argument and state-format checks, then the GPU one."""
+    from sr_states import _lib
+    from sr_states.optim.adamw import adamw_scalars
+    from sr_states.optim.sgd import sgdm_scalars
+
+    launcher = _lib.launcher()
+    bf16, e4m3 = _lib.DTYPE_CODES[torch.bfloat16], _lib.DTYPE_CODES[torch.float8_e4m3fn]
+    sr = _lib.SR_STOCHASTIC
+    p, g = torch.zeros(8), torch.zeros(8)
+    m, v = torch.zeros(8, dtype=torch.bfloat16), torch.zeros(8, dtype=torch.bfloat16)
+    scalars = adamw_scalars(1e-3, 0.9, 0.999, 1e-8, 0.01, 1)
+    assert len(scalars) == 8 and len(sgdm_scalars(1e-3, 0.9)) == 2
+
+    def adamw(*tensors, m_code=bf16):
+        return launcher.adamw_step(*tensors, m_code, sr, bf16, sr, scalars, 7, 0, 256, 0)
+
+    with pytest.raises(ValueError, match="require GPU tensors"):
+        adamw(p, g, m, v)
+    with pytest.raises(ValueError, match="state dtype does not match its state format"):
+        adamw(p, g, m, v, m_code=e4m3)
+    with pytest.raises(TypeError, match="must be tensors"):
+        adamw(p, g, m, [0.0] * 8)
+    with pytest.raises(TypeError):
+        launcher.adamw_step(p, g, m, v, bf16, sr, bf16, sr, scalars[:7], 7, 0, 256, 0)
+    with pytest.raises(ValueError, match="require GPU tensors"):
+        launcher.sgdm_step(p, g, m, bf16, sr, sgdm_scalars(1e-3, 0.9), 7, 0, 256, 0)
+    with pytest.raises(ValueError, match="state dtype does not match its state format"):
+        launcher.sgdm_step(p, g, m, e4m3, sr, sgdm_scalars(1e-3, 0.9), 7, 0, 256, 0)
+    with pytest.raises(ValueError, match="require GPU tensors"):
+        sr_states.hip_adamw_step_(p, g, m, v, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0,
+                                  step=1, seed=7)
+    with pytest.raises(ValueError, match="require GPU tensors"):
+        sr_states.hip_sgdm_step_(p, g, m, lr=1e-3, momentum_factor=0.9, seed=7)
 
 
 @pytest.mark.parametrize("arch", ["gfx950:sramecc+:xnack-", "gfx950", "gfx942:sramecc+:xnack-", "gfx90a", "gfx1100"])
