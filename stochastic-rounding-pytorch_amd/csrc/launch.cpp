@@ -46,6 +46,7 @@
 #include <cstdint>
 #include <exception>
 #include <initializer_list>
+#include <string>
 
 #include "../../include/sr_states_hip.h"
 
@@ -96,17 +97,28 @@ bool tensors(std::initializer_list<PyObject*> objects) {
   return true;
 }
 
-// Calls `launch` with `device` current; a device the guard cannot select
-// becomes a RuntimeError.
+// Calls `launch` with `device` current and the GIL released, as torch's
+// own operators and a ctypes call do (a launch can wait for room in the
+// device queue); a device the guard cannot select becomes a RuntimeError.
+// The tensors stay alive through the caller's argument tuple.
 template <class Launch>
 PyObject* on_device(const c10::Device& device, Launch launch) {
   int status = 0;
+  bool failed = false;
+  std::string message;
+  Py_BEGIN_ALLOW_THREADS
   try {
     const c10::DeviceGuard guard(device);
     status = launch();
   } catch (const std::exception& error) {
-    return fail(PyExc_RuntimeError, error.what());
+    failed = true;
+    message = error.what();
+  } catch (...) {
+    failed = true;
+    message = "unknown C++ exception in a native launch";
   }
+  Py_END_ALLOW_THREADS
+  if (failed) return fail(PyExc_RuntimeError, message.c_str());
   return PyLong_FromLong(status);
 }
 
@@ -130,6 +142,7 @@ PyObject* cast(PyObject*, PyObject* args) {
   if (n) {
     const auto x_start = reinterpret_cast<uintptr_t>(x.const_data_ptr());
     const auto out_start = reinterpret_cast<uintptr_t>(out.const_data_ptr());
+    if (!x_start || !out_start) return fail(PyExc_ValueError, "tensors without device memory cannot be cast");
     if (x_start < out_start + out.nbytes() && out_start < x_start + x.nbytes()) {
       return fail(PyExc_ValueError, "out must not overlap the input");
     }
@@ -177,6 +190,12 @@ bool check_update_tensors(std::initializer_list<const at::Tensor*> ts) {
     return false;
   }
   if (p.numel() == 0) return true;
+  for (const at::Tensor* t : ts) {
+    if (t->const_data_ptr() == nullptr) {
+      fail(PyExc_ValueError, "fused state updates require tensors that hold device memory");
+      return false;
+    }
+  }
   // Every written span (all but the gradient) disjoint from every other
   // span: with one read-only tensor, every pair holds a written one.
   int i = 0;
@@ -259,11 +278,26 @@ PyObject* sgdm_step(PyObject*, PyObject* args) {
   });
 }
 
+// Every entry behind one guard: a C++ exception from torch (a tensor
+// without storage refuses its data pointer) becomes a RuntimeError instead
+// of escaping into the interpreter.
+template <PyObject* (*Entry)(PyObject*, PyObject*)>
+PyObject* guarded(PyObject* self, PyObject* args) {
+  try {
+    return Entry(self, args);
+  } catch (const std::exception& error) {
+    return fail(PyExc_RuntimeError, error.what());
+  } catch (...) {
+    return fail(PyExc_RuntimeError, "unknown C++ exception in a native entry");
+  }
+}
+
 PyMethodDef methods[] = {
     {"bind", bind, METH_VARARGS, "Keep the addresses of the C ABI's single-tensor entry points."},
-    {"cast", cast, METH_VARARGS, "Check the tensors and call sr_cast; returns its status."},
-    {"adamw_step", adamw_step, METH_VARARGS, "Check the tensors and call sr_adamw_step; returns its status."},
-    {"sgdm_step", sgdm_step, METH_VARARGS, "Check the tensors and call sr_sgdm_step; returns its status."},
+    {"cast", guarded<cast>, METH_VARARGS, "Check the tensors and call sr_cast; returns its status."},
+    {"adamw_step", guarded<adamw_step>, METH_VARARGS,
+     "Check the tensors and call sr_adamw_step; returns its status."},
+    {"sgdm_step", guarded<sgdm_step>, METH_VARARGS, "Check the tensors and call sr_sgdm_step; returns its status."},
     {nullptr, nullptr, 0, nullptr},
 };
 

@@ -143,3 +143,46 @@ def test_cast_rejects_invalid_inputs(cuda):
         cast(torch.ones(4, device=cuda), dtype=torch.bfloat16, num_warps=3)
     with pytest.raises(ValueError, match="store_mode"):
         sr_cast_bf16(torch.ones(4, device=cuda), seed=1, store_mode="invalid")
+
+
+def test_casts_and_updates_from_several_threads(cuda):
+    """The native entries release the GIL while launching: four threads, each on
+    its own stream, cast and update their own tensors; every result equals the
+    oracle's."""
+    import threading
+
+    import sr_states
+
+    x = _inputs(torch.bfloat16)
+    options = {"dtype": torch.bfloat16, "rounding": "stochastic"}
+    gen = torch.Generator().manual_seed(17)
+    p, g = torch.randn(3001, generator=gen), torch.randn(3001, generator=gen) * 1e-2
+    m = (torch.randn(3001, generator=gen) * 1e-3).bfloat16()
+    results, errors = {}, []
+
+    def work(k):
+        try:
+            stream = torch.cuda.Stream(device=cuda)
+            with torch.cuda.stream(stream):
+                xs, ps, gs, ms = (t.to(cuda, non_blocking=False) for t in (x, p, g, m))
+                for _ in range(25):
+                    cast = sr_states.cast(xs, seed=k, **options)
+                sr_states.hip_sgdm_step_(ps, gs, ms, lr=1e-3, momentum_factor=0.9, seed=k)
+            stream.synchronize()
+            results[k] = (cast.cpu(), ps.cpu(), ms.cpu())
+        except Exception as error:  # reported below, in the test's thread
+            errors.append(error)
+
+    threads = [threading.Thread(target=work, args=(k,)) for k in range(4)]
+    for thread in threads:
+        thread.start()
+    for thread in threads:
+        thread.join(timeout=60)
+    assert not errors and len(results) == 4, errors
+    for k, (cast, ps, ms) in results.items():
+        assert_bits_or_nan(cast, sr_oracle.cast(x, seed=k, **options), f"thread {k} cast")
+        want_p, want_m = p.clone(), m.clone()
+        c_oracle.sgdm_step_(want_p, g, want_m, formats=((torch.bfloat16, "stochastic"),), seed=k,
+                            lr=1e-3, momentum_factor=0.9)
+        assert_bits_or_nan(ps, want_p, f"thread {k} parameter")
+        assert_bits_or_nan(ms, want_m, f"thread {k} momentum")

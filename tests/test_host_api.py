@@ -235,6 +235,35 @@ def test_update_entries_check_their_tensors_before_the_device():
         sr_states.hip_sgdm_step_(p, g, m, lr=1e-3, momentum_factor=0.9, seed=7)
 
 
+def test_native_entries_refuse_tensors_without_memory():
+    """A wrapper subclass on the GPU device holds no memory: refused, never launched.
+
+    Building one needs no GPU, so the refusal shows on the CPU.
+    """
+    from sr_states import _lib
+
+    class Storageless(torch.Tensor):
+        @staticmethod
+        def __new__(cls, size, dtype):
+            return torch.Tensor._make_wrapper_subclass(cls, size, dtype=dtype, device="cuda")
+
+        @classmethod
+        def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+            raise NotImplementedError(func)
+
+    launcher = _lib.launcher()
+    bf16, sr = _lib.DTYPE_CODES[torch.bfloat16], _lib.SR_STOCHASTIC
+    x, out = Storageless((16,), torch.float32), Storageless((16,), torch.bfloat16)
+    with pytest.raises(ValueError, match="without device memory"):
+        launcher.cast(x, out, bf16, sr, 0, 0, 256, 0)
+    p, g = Storageless((16,), torch.float32), Storageless((16,), torch.float32)
+    m, v = Storageless((16,), torch.bfloat16), Storageless((16,), torch.bfloat16)
+    with pytest.raises(ValueError, match="hold device memory"):
+        launcher.adamw_step(p, g, m, v, bf16, sr, bf16, sr, (0.0,) * 8, 0, 0, 256, 0)
+    with pytest.raises(ValueError, match="hold device memory"):
+        launcher.sgdm_step(p, g, m, bf16, sr, (0.0, 0.0), 0, 0, 256, 0)
+
+
 @pytest.mark.parametrize("arch", ["gfx950:sramecc+:xnack-", "gfx950", "gfx942:sramecc+:xnack-", "gfx90a", "gfx1100"])
 def test_device_check_accepts_only_the_built_architecture(monkeypatch, arch):
     """tests/test_fp8_storage.py:88-108, with the gfx950 check in place of sm_89.
