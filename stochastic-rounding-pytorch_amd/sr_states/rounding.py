@@ -30,20 +30,28 @@ _ROUTINES: dict[tuple[torch.dtype, str], _Routine] = {}
 _BACKENDS = ("reference", "hip")
 
 
-def register_rounding(name: str, dtype: torch.dtype, *, reference: Callable) -> None:
-    """Register a rounding rule for one storage dtype.
+def register_rounding(
+    name: str, dtype: torch.dtype, *, reference: Callable, triton: Callable | None = None
+) -> None:
+    """Register a rounding rule for one storage dtype (sr_states/rounding.py:28-67).
 
     ``reference(x, *, dtype, seed, offset)`` receives FP32 values and returns a
     tensor of ``dtype`` with the same shape and device without mutating ``x``.
     Names and dtypes are stored in checkpoints; callables are not.  Replacing a
     registration is forbidden.  Rules registered here have no HIP
-    implementation, so fused HIP optimizers reject them.
+    implementation, so fused HIP optimizers reject them; ``cast`` and the
+    per-parameter optimizers apply ``reference``.
+
+    ``triton`` is the reference's optional Triton callback for its fused
+    kernels.  It is accepted so that registrations written for the reference
+    run unchanged, checked to be callable as the reference checks it, and
+    not used: there is no Triton JIT in this backend.
     """
     if not isinstance(name, str) or not name:
         raise ValueError("rounding name must be a nonempty string")
     if not isinstance(dtype, torch.dtype) or not dtype.is_floating_point:
         raise ValueError("dtype must be a floating-point torch.dtype")
-    if not callable(reference):
+    if not callable(reference) or (triton is not None and not callable(triton)):
         raise TypeError("rounding implementations must be callable")
     key = (dtype, name)
     if key in _ROUTINES:

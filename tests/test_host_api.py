@@ -137,6 +137,34 @@ def test_registration_validation_and_builtins():
         validate_rounding(torch.bfloat16, "nearest", backend="unknown")
 
 
+def test_registrations_with_a_triton_callback_run_unchanged():
+    """tests/test_triton_rounding_extensions.py:32-43: ``triton=`` is accepted, checked and unused.
+
+    The rule then behaves as any registered rule without a HIP implementation:
+    the fused optimizers refuse it by name, the per-parameter ones and
+    ``cast`` take it (the GPU tests run them).
+    """
+
+    def callback(value, counter, dtype):
+        raise AssertionError("the Triton callback is never called")
+
+    with pytest.raises(TypeError, match="callable"):
+        register_rounding("toward_zero", torch.bfloat16, reference=toward_zero, triton=5)
+    register_rounding("toward_zero", torch.bfloat16, reference=toward_zero, triton=callback)
+    register_rounding("custom_nearest", torch.float16, reference=lambda x, **kw: x.to(kw["dtype"]),
+                      triton=callback)
+    validate_rounding(torch.bfloat16, "toward_zero")
+    with pytest.raises(ValueError, match="no HIP implementation"):
+        validate_rounding(torch.bfloat16, "toward_zero", backend="hip")
+    p = torch.nn.Parameter(torch.ones(4))
+    with pytest.raises(ValueError, match="no HIP implementation"):
+        AdamWHip([p], lr=0.01, rounding="toward_zero")
+    with pytest.raises(ValueError, match="no HIP implementation"):
+        SGDMHip([p], lr=0.01, state_dtype=torch.float16, rounding="custom_nearest")
+    for cls in (AdamWReferenceSR, SGDMReferenceSR):
+        cls([p], lr=0.01, rounding="toward_zero")
+
+
 def test_custom_rule_cast_contract():
     """tests/test_rounding_registry.py:131-139: custom routines run as registered."""
     register_rounding("toward_zero", torch.bfloat16, reference=toward_zero)
