@@ -268,6 +268,21 @@ WORKLOADS = {
         steps=2000,
         warmup=5000,
     ),
+    # Host time per call of the single-tensor entries (1024 elements, BF16-SR
+    # states) and per step of the optimizers on GPT-2's shapes, beside
+    # torch's fused AdamW and conversion: not an optimizer step.
+    "host_costs": dict(
+        optimizer="host",
+        shapes=[(1024,)],
+        p_dtype=torch.float32,
+        g_dtype=torch.float32,
+        formats=((torch.bfloat16, "stochastic"), (torch.bfloat16, "stochastic")),
+        grad_std=1e-3,
+        hparams=dict(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=1e-2),
+        seed=7,
+        steps=2000,
+        warmup=200,
+    ),
     # Config 5: gradients with 5% exact zeros, 1% of magnitude below 2^-14
     # (FP16 subnormal range) and the rest N(0, 1e-2).
     "c5_sgdm_fp16": dict(
@@ -626,6 +641,79 @@ def cast_sizes(spec, steps, warmup):
     return rows
 
 
+def host_costs(spec, steps, warmup):
+    """Host time per call of the single-tensor entries and per optimizer step.
+
+    Each entry runs ``warmup`` untimed calls, then ``steps`` back-to-back
+    calls (a tenth as many for the GPT-2 optimizer steps) with Python's
+    cyclic garbage collector paused, so that one collection over torch's
+    objects (tens of milliseconds) does not land in one entry's average.
+    ``host_us`` is the time for the calls to return; ``device_us`` spans the
+    same calls between two events on the current stream, so it equals
+    ``host_us`` when the host bounds the rate and exceeds it otherwise.
+    """
+    import gc
+
+    import sr_states
+    import sr_states.reference as functional
+    from sr_states.hip.adamw import hip_adamw_step_
+    from sr_states.hip.sgd import hip_sgdm_step_
+
+    device = torch.device("cuda", 0)
+    gen = torch.Generator(device=device).manual_seed(spec["seed"])
+    (n,) = spec["shapes"][0]
+    p = torch.empty(n, device=device).normal_(generator=gen)
+    g = torch.empty(n, device=device).normal_(generator=gen) * spec["grad_std"]
+    m = torch.zeros(n, device=device, dtype=torch.bfloat16)
+    v = torch.zeros(n, device=device, dtype=torch.bfloat16)
+    x = torch.empty(n, device=device).normal_(generator=gen)
+    hp = {**spec["hparams"], "step": 3}
+    sgd = {"lr": hp["lr"], "momentum_factor": 0.9}
+    shapes = WORKLOADS["c3_gpt2"]["shapes"]
+
+    def gpt2_params():
+        params = [torch.nn.Parameter(torch.empty(s, device=device).normal_(generator=gen) * 0.02) for s in shapes]
+        for q in params:
+            q.grad = torch.empty_like(q).normal_(generator=gen) * spec["grad_std"]
+        return params
+
+    torch_params = gpt2_params()
+    torch_adamw = torch.optim.AdamW(torch_params, lr=hp["lr"], fused=True)
+    entries = {
+        "hip_adamw_step_": (lambda: hip_adamw_step_(p, g, m, v, seed=7, **hp), 1),
+        "hip_sgdm_step_": (lambda: hip_sgdm_step_(p, g, m, seed=7, **sgd), 1),
+        "reference.adamw_step_": (lambda: functional.adamw_step_(p, g, m, v, seed=7, **hp), 1),
+        "reference.sgdm_step_": (lambda: functional.sgdm_step_(p, g, m, seed=7, **sgd), 1),
+        "sr_states.cast (BF16 SR)": (lambda: sr_states.cast(x, dtype=torch.bfloat16, seed=7), 1),
+        "torch: x.to(bfloat16)": (lambda: x.to(torch.bfloat16), 1),
+        "AdamWHip.step (GPT-2, 148 tensors)": (sr_states.AdamWHip(gpt2_params(), lr=hp["lr"]).step, 10),
+        "AdamWReferenceSR.step (GPT-2, 148 tensors)": (sr_states.AdamWReferenceSR(gpt2_params(), lr=hp["lr"]).step, 10),
+        "torch.optim.AdamW(fused=True).step (GPT-2, FP32 states)": (torch_adamw.step, 10),
+    }
+    rows = []
+    for name, (call, divisor) in entries.items():
+        count = max(1, steps // divisor)
+        for _ in range(max(1, warmup // divisor)):
+            call()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        gc.collect()
+        gc.disable()
+        try:
+            start.record()
+            began = time.perf_counter_ns()
+            for _ in range(count):
+                call()
+            returned = time.perf_counter_ns()
+            end.record()
+            torch.cuda.synchronize()
+        finally:
+            gc.enable()
+        rows.append({"entry": name, "calls": count, "host_us": (returned - began) / count / 1e3,
+                     "device_us": start.elapsed_time(end) * 1e3 / count})
+    return rows
+
+
 def _median_step_seconds(opt, target_seconds: float, min_steps: int = 3) -> tuple[float, int]:
     opt.step()  # allocate states
     times = []
@@ -897,6 +985,16 @@ def main():
             "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded normal draws on the GPU)",
             "note": "value = the stochastic cast at the largest size; rows hold every size and method",
             "peak": HBM_PEAK_GBPS, "sizes": rows}), flush=True)
+        return
+    if spec["optimizer"] == "host":
+        rows = host_costs(spec, args.steps, args.warmup)
+        print(json.dumps({
+            "metric": "host time per call of the single-tensor entries and per optimizer step, 1 MI355X",
+            "value": rows[0]["host_us"], "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "higher_is_better": False, "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (seeded normal draws on the GPU)",
+            "note": "value = hip_adamw_step_ on 1024 elements; rows hold every entry",
+            "entries": rows}), flush=True)
         return
     work = build(spec, device)
     step = work.step

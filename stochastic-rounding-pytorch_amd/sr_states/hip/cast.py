@@ -32,7 +32,7 @@ def native_cast(x, *, dtype, rule, seed=0, offset=0, threads=_DEFAULT_THREADS, o
     if device.type != "cuda":
         raise ValueError(f"sr_states casts run on the GPU; got a {device.type} tensor")
     validate_device(device)
-    output = torch.empty(x.shape, dtype=dtype, device=device) if out is None else out
+    output = torch.empty_like(x, dtype=dtype, memory_format=torch.contiguous_format) if out is None else out
     # The native entry checks `output` (dtype, shape, device, contiguity and
     # no byte shared with x), then calls sr_cast with x's device current.
     status = _lib.launcher().cast(x, output, _lib.DTYPE_CODES[dtype], rule, _lib.low32(seed),

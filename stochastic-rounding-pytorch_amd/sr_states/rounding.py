@@ -106,6 +106,13 @@ def cast(
     """
     if x.dtype != torch.float32:
         raise TypeError(f"expected torch.float32 input, got {x.dtype}")
+    try:
+        routine = _ROUTINES.get((dtype, rounding))
+    except TypeError:  # an unhashable rule: validate_rounding names the error
+        routine = None
+    if routine is not None and routine.native is not None:
+        # A built-in rule: the HIP cast returns x's shape and device in dtype.
+        return routine.reference(x, dtype=dtype, seed=seed, offset=offset)
     validate_rounding(dtype, rounding)
     result = _ROUTINES[dtype, rounding].reference(x, dtype=dtype, seed=seed, offset=offset)
     if not isinstance(result, torch.Tensor):
@@ -118,12 +125,16 @@ def cast(
 
 
 def _builtin(code: int, rule: int) -> Callable:
-    def routine(x, *, dtype, seed, offset):
-        if code == _lib.SR_F32:
+    if code == _lib.SR_F32:
+        def routine(x, *, dtype, seed, offset):
             return x
-        from .hip.cast import native_cast
+    else:
+        def routine(x, *, dtype, seed, offset):
+            # Imported here: sr_states.hip imports this module.
+            from .hip.cast import native_cast
 
-        return native_cast(x.contiguous(), dtype=dtype, rule=rule, seed=seed, offset=offset)
+            return native_cast(x if x.is_contiguous() else x.contiguous(), dtype=dtype, rule=rule,
+                               seed=seed, offset=offset)
 
     routine.__name__ = f"hip_cast_{code}_{rule}"
     return routine
