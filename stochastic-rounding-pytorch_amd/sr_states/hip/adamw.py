@@ -86,12 +86,44 @@ def hip_adamw_step_(
     ``seed`` is the update key and ``offset`` the flat index of the first
     element.
     """
-    (m_code, m_rule), (v_code, v_rule) = resolve_native_codes(
-        _STATE_NAMES, (exp_avg, exp_avg_sq), formats, rounding, block_size
-    )
+    codes = resolve_native_codes(_STATE_NAMES, (exp_avg, exp_avg_sq), formats, rounding, block_size)
     _validate_hyperparameters(lr, (beta1, beta2), eps, weight_decay)
+    _launch_step(parameter, gradient, exp_avg, exp_avg_sq, codes,
+                 adamw_scalars(lr, beta1, beta2, eps, weight_decay, _positive_step(step)), seed, offset, block_size)
+
+
+@torch.no_grad()
+def adamw_step_any_hyperparameters_(
+    parameter, gradient, exp_avg, exp_avg_sq, *, lr, beta1, beta2, eps, weight_decay, step, seed=0, offset=0,
+    formats=None,
+):
+    """``hip_adamw_step_`` for the reference's functional updates, which check no hyperparameter.
+
+    sr_states/reference/adamw.py:54-105 computes with any learning rate,
+    epsilon, weight decay and betas; so does this.  The one limit is the
+    launch's: the division by sqrt(1 - beta2^step) is exact for constants
+    in [2^-27, 1], which every beta2 in [0, 1) gives, and the library
+    refuses others with an error.  beta1 = 1 divides by zero here as in the
+    reference.
+    """
+    codes = resolve_native_codes(_STATE_NAMES, (exp_avg, exp_avg_sq), formats, None, DEFAULT_BLOCK_SIZE)
+    scalars = adamw_scalars(lr, beta1, beta2, eps, weight_decay, _positive_step(step))
+    correction = scalars[5]  # sqrt(1 - beta2**step): complex when beta2**step > 1
+    if isinstance(correction, complex) or not 0 < correction <= 1:
+        raise ValueError(
+            f"sqrt(1 - beta2**step) must lie in (0, 1] for the fused update; got beta2={beta2}, step={step}"
+        )
+    _launch_step(parameter, gradient, exp_avg, exp_avg_sq, codes, scalars, seed, offset, DEFAULT_BLOCK_SIZE)
+
+
+def _positive_step(step):
     if not isinstance(step, int) or isinstance(step, bool) or step < 1:
         raise ValueError("step must be a positive integer")
+    return step
+
+
+def _launch_step(parameter, gradient, exp_avg, exp_avg_sq, codes, scalars, seed, offset, block_size):
+    (m_code, m_rule), (v_code, v_rule) = codes
     reject_dtensors(parameter, gradient, exp_avg, exp_avg_sq)
     device = parameter.device
     if device.type != "cuda":
@@ -100,9 +132,8 @@ def hip_adamw_step_(
     # The native entry checks devices, shapes, layout, dtypes and overlap with
     # the messages of sr_states/triton/_optimizer.py:24-60, then launches.
     status = _lib.launcher().adamw_step(
-        parameter, gradient, exp_avg, exp_avg_sq, m_code, m_rule, v_code, v_rule,
-        adamw_scalars(lr, beta1, beta2, eps, weight_decay, step), _lib.low32(seed), _lib.low32(offset), block_size,
-        _lib.stream_handle(device),
+        parameter, gradient, exp_avg, exp_avg_sq, m_code, m_rule, v_code, v_rule, scalars, _lib.low32(seed),
+        _lib.low32(offset), block_size, _lib.stream_handle(device),
     )
     _lib.check("sr_adamw_step", status)
 

@@ -65,10 +65,28 @@ def hip_sgdm_step_(
     any built-in storage format.  ``seed`` is the update key and ``offset``
     the flat index of the first element.
     """
-    ((code, rule),) = resolve_native_codes(_STATE_NAMES, (momentum,), formats, rounding, block_size)
+    codes = resolve_native_codes(_STATE_NAMES, (momentum,), formats, rounding, block_size)
     nonnegative("learning rate", lr)
     if not 0 <= momentum_factor < 1:
         raise ValueError(f"invalid momentum value: {momentum_factor}")
+    _launch_step(parameter, gradient, momentum, codes, sgdm_scalars(lr, momentum_factor), seed, offset, block_size)
+
+
+@torch.no_grad()
+def sgdm_step_any_hyperparameters_(parameter, gradient, momentum, *, lr, momentum_factor, seed=0, offset=0,
+                                   formats=None):
+    """``hip_sgdm_step_`` for the reference's functional updates, which check no hyperparameter.
+
+    sr_states/reference/sgd.py:44-72 computes with any learning rate and
+    momentum factor; so does this.
+    """
+    codes = resolve_native_codes(_STATE_NAMES, (momentum,), formats, None, DEFAULT_BLOCK_SIZE)
+    _launch_step(parameter, gradient, momentum, codes, sgdm_scalars(lr, momentum_factor), seed, offset,
+                 DEFAULT_BLOCK_SIZE)
+
+
+def _launch_step(parameter, gradient, momentum, codes, scalars, seed, offset, block_size):
+    ((code, rule),) = codes
     reject_dtensors(parameter, gradient, momentum)
     device = parameter.device
     if device.type != "cuda":
@@ -77,8 +95,8 @@ def hip_sgdm_step_(
     # The native entry checks devices, shapes, layout, dtypes and overlap with
     # the messages of sr_states/triton/_optimizer.py:24-60, then launches.
     status = _lib.launcher().sgdm_step(
-        parameter, gradient, momentum, code, rule, sgdm_scalars(lr, momentum_factor), _lib.low32(seed),
-        _lib.low32(offset), block_size, _lib.stream_handle(device),
+        parameter, gradient, momentum, code, rule, scalars, _lib.low32(seed), _lib.low32(offset), block_size,
+        _lib.stream_handle(device),
     )
     _lib.check("sr_sgdm_step", status)
 

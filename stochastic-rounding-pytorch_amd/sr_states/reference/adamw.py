@@ -9,9 +9,10 @@ with the parameter computed from the unrounded FP32 moments, rounded to its
 own dtype (nearest even), and each moment stored through its format with
 counter base ``state_key(seed, k)`` and shard start ``offset``.
 
-Hyperparameters must lie where the optimizers accept them (non-negative
-``lr``, ``eps`` and ``weight_decay``, betas in [0, 1)); the eager reference
-computes with any value.
+Like the reference, they check no hyperparameter: any learning rate,
+epsilon and weight decay are taken (a negative learning rate ascends).  The
+one limit is the launch's exact division by sqrt(1 - beta2**step), which
+takes every beta2 in [0, 1); beta1 = 1 divides by zero as in the reference.
 """
 
 from __future__ import annotations
@@ -19,7 +20,7 @@ from __future__ import annotations
 import torch
 
 from ..formats import resolve_formats
-from ..hip.adamw import hip_adamw_step_
+from ..hip.adamw import adamw_step_any_hyperparameters_
 from ._functional import update_in_place, updated
 
 _NAMES = ("exp_avg", "exp_avg_sq")
@@ -61,8 +62,8 @@ def adamw_step(
     resolved = _formats(step, state_dtype, formats, rounding)
     return tuple(
         updated(
-            hip_adamw_step_, parameter, gradient, (exp_avg, exp_avg_sq), resolved, seed=seed, offset=offset,
-            lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, step=step,
+            adamw_step_any_hyperparameters_, parameter, gradient, (exp_avg, exp_avg_sq), resolved, seed=seed,
+            offset=offset, lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, step=step,
         )
     )
 
@@ -94,6 +95,6 @@ def adamw_step_(
     """
     resolved = _formats(step, state_dtype, formats, rounding)
     update_in_place(
-        hip_adamw_step_, parameter, gradient, (exp_avg, exp_avg_sq), resolved, seed=seed, offset=offset,
-        lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, step=step,
+        adamw_step_any_hyperparameters_, parameter, gradient, (exp_avg, exp_avg_sq), resolved, seed=seed,
+        offset=offset, lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, step=step,
     )

@@ -7,8 +7,8 @@ gfx950 and take GPU tensors only: ``u' = fma(momentum_factor, u, g)``,
 its own dtype (nearest even) and the momentum stored through its format with
 counter base ``state_key(seed, 0)`` and shard start ``offset``.
 
-``lr`` must be non-negative and ``momentum_factor`` in [0, 1), the range
-the optimizers accept; the eager reference computes with any value.
+Like the reference, they check no hyperparameter: any ``lr`` and
+``momentum_factor`` are taken.
 """
 
 from __future__ import annotations
@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 
 from ..formats import resolve_formats
-from ..hip.sgd import hip_sgdm_step_
+from ..hip.sgd import sgdm_step_any_hyperparameters_
 from ._functional import update_in_place, updated
 
 _NAMES = ("momentum_buffer",)
@@ -44,7 +44,7 @@ def sgdm_step(
     resolved = resolve_formats(_NAMES, formats, state_dtype=state_dtype, rounding=rounding)
     return tuple(
         updated(
-            hip_sgdm_step_, parameter, gradient, (momentum,), resolved, seed=seed, offset=offset,
+            sgdm_step_any_hyperparameters_, parameter, gradient, (momentum,), resolved, seed=seed, offset=offset,
             lr=lr, momentum_factor=momentum_factor,
         )
     )
@@ -67,6 +67,6 @@ def sgdm_step_(
     """Apply the update in place, including state write-back (reference/sgd.py:75-84)."""
     resolved = resolve_formats(_NAMES, formats, state_dtype=state_dtype, rounding=rounding)
     update_in_place(
-        hip_sgdm_step_, parameter, gradient, (momentum,), resolved, seed=seed, offset=offset,
+        sgdm_step_any_hyperparameters_, parameter, gradient, (momentum,), resolved, seed=seed, offset=offset,
         lr=lr, momentum_factor=momentum_factor,
     )

@@ -312,3 +312,59 @@ def test_registered_rules_are_applied_by_the_functional_and_eager_updates(cuda):
     assert_bits_or_nan(params[0].detach().cpu(), c_p, "eager parameter")
     assert_bits_or_nan(state["exp_avg"].cpu(), _toward_zero(c_m, dtype=torch.bfloat16, seed=0, offset=0), "m")
     assert_bits_or_nan(state["exp_avg_sq"].cpu(), _toward_zero(c_v, dtype=torch.bfloat16, seed=0, offset=0), "v")
+
+
+@pytest.mark.parametrize("hyper", [
+    {"lr": -1e-3},
+    {"weight_decay": -0.05},
+    {"eps": -1e-3},
+    {"beta1": 1.25, "beta2": 0.0},
+    {"beta1": -0.5, "lr": 2.0, "weight_decay": 3.0},
+], ids=lambda h: ",".join(f"{k}={v}" for k, v in h.items()))
+def test_reference_adamw_takes_any_hyperparameters_as_the_reference_does(cuda, hyper):
+    """reference/adamw.py:54-105 checks no hyperparameter; nor does sr_states.reference.
+
+    Values the optimizers refuse (a negative learning rate, epsilon or
+    weight decay; betas outside [0, 1)) update as the C oracle does, byte
+    for byte; a negative epsilon makes some denominators negative.
+    """
+    formats = FORMAT_SETS[1]
+    options = {**ADAMW, **hyper}
+    p, g, (m, v) = _inputs(3001, torch.float32, torch.float32, [f[0] for f in formats], seed=21)
+    want = [t.clone() for t in (p, g, m, v)]
+    c_oracle.adamw_step_(*want, formats=formats, seed=KEY, offset=OFFSET, **options)
+    got = [t.to(cuda) for t in (p, g, m, v)]
+    functional.adamw_step_(*got, formats=_fmts(formats), seed=KEY, offset=OFFSET, **options)
+    _assert_all([got[0], got[2], got[3]], [want[0], want[2], want[3]], f"adamw_step_ {hyper}")
+    out = functional.adamw_step(*(t.to(cuda) for t in (p, g, m, v)), formats=_fmts(formats), seed=KEY,
+                                offset=OFFSET, **options)
+    _assert_all(out, [want[0], want[2], want[3]], f"adamw_step {hyper}")
+    with pytest.raises(ValueError, match="invalid"):
+        sr_states.hip_adamw_step_(*got, formats=_fmts(formats), seed=KEY, offset=OFFSET, **options)
+
+
+def test_reference_adamw_refuses_only_what_the_launch_cannot_divide_by(cuda):
+    p, g, (m, v) = _inputs(64, torch.float32, torch.float32, [torch.bfloat16] * 2)
+    p, g, m, v = (t.to(cuda) for t in (p, g, m, v))
+    for beta2 in (1.0, 1.5, -3.0):
+        with pytest.raises(ValueError, match=r"sqrt\(1 - beta2\*\*step\)"):
+            functional.adamw_step_(p, g, m, v, **{**ADAMW, "beta2": beta2, "step": 1})
+    with pytest.raises(ZeroDivisionError):  # 1 - beta1**step == 0, as in the reference
+        functional.adamw_step_(p, g, m, v, **{**ADAMW, "beta1": 1.0})
+
+
+@pytest.mark.parametrize("hyper", [{"lr": -0.01}, {"momentum_factor": 1.0}, {"momentum_factor": -0.9, "lr": 3.0},
+                                   {"momentum_factor": 1.5}],
+                         ids=lambda h: ",".join(f"{k}={v}" for k, v in h.items()))
+def test_reference_sgdm_takes_any_hyperparameters_as_the_reference_does(cuda, hyper):
+    """reference/sgd.py:44-72 checks no hyperparameter; nor does sr_states.reference."""
+    formats = ((torch.float8_e4m3fn, "stochastic"),)
+    options = {**SGDM, **hyper}
+    p, g, (u,) = _inputs(3001, torch.bfloat16, torch.float32, [formats[0][0]], seed=22)
+    want = [t.clone() for t in (p, g, u)]
+    c_oracle.sgdm_step_(*want, formats=formats, seed=KEY, offset=OFFSET, **options)
+    got = [t.to(cuda) for t in (p, g, u)]
+    functional.sgdm_step_(*got, formats=_fmts(formats), seed=KEY, offset=OFFSET, **options)
+    _assert_all([got[0], got[2]], [want[0], want[2]], f"sgdm_step_ {hyper}")
+    with pytest.raises(ValueError, match="invalid"):
+        sr_states.hip_sgdm_step_(*got, formats=_fmts(formats), seed=KEY, offset=OFFSET, **options)
