@@ -92,7 +92,6 @@ def hip_adamw_step_(
                  adamw_scalars(lr, beta1, beta2, eps, weight_decay, _positive_step(step)), seed, offset, block_size)
 
 
-@torch.no_grad()
 def adamw_step_any_hyperparameters_(
     parameter, gradient, exp_avg, exp_avg_sq, *, lr, beta1, beta2, eps, weight_decay, step, seed=0, offset=0,
     formats=None,
@@ -104,7 +103,8 @@ def adamw_step_any_hyperparameters_(
     launch's: the division by sqrt(1 - beta2^step) is exact for constants
     in [2^-27, 1], which every beta2 in [0, 1) gives, and the library
     refuses others with an error.  beta1 = 1 divides by zero here as in the
-    reference.
+    reference.  Its callers run under no_grad; the launch itself records
+    nothing for autograd.
     """
     codes = resolve_native_codes(_STATE_NAMES, (exp_avg, exp_avg_sq), formats, None, DEFAULT_BLOCK_SIZE)
     scalars = adamw_scalars(lr, beta1, beta2, eps, weight_decay, _positive_step(step))

@@ -72,13 +72,13 @@ def hip_sgdm_step_(
     _launch_step(parameter, gradient, momentum, codes, sgdm_scalars(lr, momentum_factor), seed, offset, block_size)
 
 
-@torch.no_grad()
 def sgdm_step_any_hyperparameters_(parameter, gradient, momentum, *, lr, momentum_factor, seed=0, offset=0,
                                    formats=None):
     """``hip_sgdm_step_`` for the reference's functional updates, which check no hyperparameter.
 
     sr_states/reference/sgd.py:44-72 computes with any learning rate and
-    momentum factor; so does this.
+    momentum factor; so does this.  Its callers run under no_grad; the
+    launch itself records nothing for autograd.
     """
     codes = resolve_native_codes(_STATE_NAMES, (momentum,), formats, None, DEFAULT_BLOCK_SIZE)
     _launch_step(parameter, gradient, momentum, codes, sgdm_scalars(lr, momentum_factor), seed, offset,

@@ -28,7 +28,7 @@ import torch
 
 from .._hash import state_key
 from ..formats import StateFormat
-from ..optim._dtensor import is_dtensor
+from ..optim._dtensor import DTensor
 from ..rounding import cast, has_native
 
 _KERNEL_DTYPES = (torch.float32, torch.bfloat16)
@@ -40,7 +40,7 @@ def check_inputs(tensors) -> None:
     if not all(isinstance(tensor, torch.Tensor) for tensor in tensors):
         raise TypeError("parameter, gradient and states must be tensors")
     for tensor in tensors:
-        if is_dtensor(tensor):
+        if DTensor is not None and isinstance(tensor, DTensor):
             raise TypeError(
                 "functional state updates take local tensors: pass each DTensor's to_local() and "
                 "the flat index of the shard's first element as offset"
