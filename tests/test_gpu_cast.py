@@ -145,6 +145,38 @@ def test_cast_rejects_invalid_inputs(cuda):
         sr_cast_bf16(torch.ones(4, device=cuda), seed=1, store_mode="invalid")
 
 
+def test_cast_into_an_output_buffer(cuda):
+    """native_cast(out=...) writes the oracle's bytes into a given buffer and
+    refuses, without writing, outputs on another device, of another shape or
+    dtype, strided, or sharing a byte with the input."""
+    from sr_states import _lib
+    from sr_states.hip.cast import native_cast
+
+    x = _inputs(torch.bfloat16).to(cuda)
+    sr = _lib.RULE_CODES["stochastic"]
+    expected = sr_oracle.cast(x.cpu(), dtype=torch.bfloat16, rounding="stochastic", seed=9, offset=4)
+    out = torch.full(x.shape, 7.0, device=cuda, dtype=torch.bfloat16)
+    assert native_cast(x, dtype=torch.bfloat16, rule=sr, seed=9, offset=4, out=out) is out
+    assert_bits_or_nan(out, expected, "into out")
+    bad = [torch.empty(x.shape, dtype=torch.bfloat16),  # host memory
+           torch.empty(x.numel() - 1, device=cuda, dtype=torch.bfloat16),
+           torch.empty(x.shape, device=cuda, dtype=torch.float16),
+           torch.empty(2 * x.numel(), device=cuda, dtype=torch.bfloat16)[::2]]
+    for candidate in bad:
+        before = candidate.clone()
+        with pytest.raises(ValueError, match="contiguous tensor of the requested dtype, shape and device"):
+            native_cast(x, dtype=torch.bfloat16, rule=sr, seed=9, out=candidate)
+        assert torch.equal(candidate.contiguous().view(torch.uint8), before.contiguous().view(torch.uint8))
+    storage = torch.zeros(2 * x.numel(), device=cuda)
+    inside = storage[: x.numel()]
+    inside.copy_(x)
+    overlapping = storage[x.numel() // 2:].view(torch.bfloat16)[: x.numel()]
+    before = storage.clone()
+    with pytest.raises(ValueError, match="overlap"):
+        native_cast(inside, dtype=torch.bfloat16, rule=sr, seed=9, out=overlapping)
+    assert torch.equal(storage.view(torch.int32), before.view(torch.int32))  # bits: x holds NaNs
+
+
 def test_casts_and_updates_from_several_threads(cuda):
     """The native entries release the GIL while launching: four threads, each on
     its own stream, cast and update their own tensors; every result equals the
