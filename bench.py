@@ -516,7 +516,7 @@ def torch_fused_baseline(spec, work, steps, warmup):
     The reference's step benchmark times ``torch.optim.AdamW`` / ``SGD`` with
     ``fused=True`` beside its own optimizers and reports the speedup
     (benchmarks/bench_optimizer_steps.py:247-251, 440-449).  Here the same
-    parameters and gradients (FP32 only: torch's fused kernels take
+    parameters and gradients (of one dtype: torch's fused kernels take
     gradients of the parameters' dtype) are stepped by torch's kernels after
     the fused SR steps are timed and read back; the time per step comes from
     two events around back-to-back steps, as for the product.  torch keeps
