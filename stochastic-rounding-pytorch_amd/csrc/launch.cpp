@@ -34,9 +34,10 @@
 //   launched; nothing is launched for empty tensors.
 //
 // Each entry calls the C ABI with the first tensor's device current (set and
-// restored only when it is not) and returns its status.  seed, key and
-// offset are taken modulo 2^32; `stream` is the raw handle of a stream on
-// that device.
+// restored only when it is not) and the GIL released, and returns its
+// status.  Non-empty tensors without device memory (wrapper subclasses) are
+// refused with ValueError.  seed, key and offset are taken modulo 2^32;
+// `stream` is the raw handle of a stream on that device.
 
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
