@@ -248,7 +248,8 @@ int sr_cast(const void* x, void* y, int64_t n, int dtype, int rule, uint32_t see
   a.counter_base = seed + offset;
   a.vector_ok = aligned16(x) && aligned16(y);
   if (int rc = tiles_for(n, block_size, sr::kCastLaneElements, &a.total_tiles)) return rc;
-  return launch(tables().cast[enc], block_size, a.total_tiles, &a, stream);
+  const bool cached_loads = n <= sr::kCachedCastMaxElements;
+  return launch(tables().cast[cached_loads][enc], block_size, a.total_tiles, &a, stream);
 }
 
 int sr_neighbors(const void* x, void* lower, void* upper, int64_t n, int dtype, void* stream) {

@@ -15,7 +15,8 @@ void fill_sgdm(KernelTableSgdm& t, std::integer_sequence<int, UE...>) {
 
 template <int... E>
 void fill_cast(KernelTableCast& t, std::integer_sequence<int, E...>) {
-  ((t[E] = reinterpret_cast<const void*>(&cast_kernel<E>)), ...);
+  ((t[0][E] = reinterpret_cast<const void*>(&cast_kernel<E, false>)), ...);
+  ((t[1][E] = reinterpret_cast<const void*>(&cast_kernel<E, true>)), ...);
 }
 
 }  // namespace
