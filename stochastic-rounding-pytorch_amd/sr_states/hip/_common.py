@@ -18,7 +18,8 @@ def is_hip_available() -> bool:
 
 @cache
 def _device_arch(device: torch.device) -> str:
-    return torch.cuda.get_device_properties(device).gcnArchName
+    """The device's architecture without its feature suffixes (gfx950 of gfx950:sramecc+:xnack-)."""
+    return torch.cuda.get_device_properties(device).gcnArchName.split(":")[0]
 
 
 def validate_device(device: torch.device) -> None:
@@ -27,7 +28,7 @@ def validate_device(device: torch.device) -> None:
         device = torch.device(device)
     if device.type != "cuda":
         raise ValueError("fused state updates require GPU tensors")
-    arch = _device_arch(device).split(":")[0]
+    arch = _device_arch(device)
     if arch != SUPPORTED_ARCH:
         raise ValueError(f"the sr_states HIP library is built for {SUPPORTED_ARCH}, not {arch}")
 

@@ -35,9 +35,10 @@ def native_cast(x, *, dtype, rule, seed=0, offset=0, threads=_DEFAULT_THREADS, o
     output = torch.empty_like(x, dtype=dtype, memory_format=torch.contiguous_format) if out is None else out
     # The native entry checks `output` (dtype, shape, device, contiguity and
     # no byte shared with x), then calls sr_cast with x's device current.
-    status = _lib.launcher().cast(x, output, _lib.DTYPE_CODES[dtype], rule, _lib.low32(seed),
-                                  _lib.low32(offset), threads, _lib.stream_handle(device))
-    _lib.check("sr_cast", status)
+    status = _lib.launcher().cast(x, output, _lib.DTYPE_CODES[dtype], rule, int(seed) & 0xFFFFFFFF,
+                                  int(offset) & 0xFFFFFFFF, threads, _lib.stream_handle(device))
+    if status:
+        _lib.check("sr_cast", status)
     return output
 
 
