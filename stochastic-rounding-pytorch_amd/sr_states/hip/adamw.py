@@ -203,9 +203,13 @@ class AdamWHip(StateOptimizer):
         )
 
     def _step_group(self, group, formats, items, rng_step):
-        launches, record_steps = prepare_group(
-            self, group, formats, items, validate_update_device
+        self._launch_prepared(
+            group, formats, prepare_group(self, group, formats, items, validate_update_device), rng_step
         )
+
+    def _launch_prepared(self, group, formats, prepared, rng_step):
+        """Queue the launches ``prepare_group`` returned, then record the steps."""
+        launches, record_steps = prepared
         beta1, beta2 = group["betas"]
         (m_code, m_rule), (v_code, v_rule) = (native_codes(f.dtype, f.rounding) for f in formats)
         seed, rng_word = _lib.low64(group["sr_seed"]), _lib.low64(rng_step)

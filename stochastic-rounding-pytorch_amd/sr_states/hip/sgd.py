@@ -153,9 +153,13 @@ class SGDMHip(StateOptimizer):
         )
 
     def _step_group(self, group, formats, items, rng_step):
-        launches, record_steps = prepare_group(
-            self, group, formats, items, validate_update_device
+        self._launch_prepared(
+            group, formats, prepare_group(self, group, formats, items, validate_update_device), rng_step
         )
+
+    def _launch_prepared(self, group, formats, prepared, rng_step):
+        """Queue the launches ``prepare_group`` returned, then record the steps."""
+        launches, record_steps = prepared
         code, rule = native_codes(formats[0].dtype, formats[0].rounding)
         hparams = sgdm_hparams(group["lr"], group["momentum"])
         seed, rng_word = _lib.low64(group["sr_seed"]), _lib.low64(rng_step)

@@ -2,25 +2,84 @@
 
 ``AdamWReferenceSR``/``AdamWReferenceRN`` (sr_states/optim/adamw.py:21-79)
 and ``SGDMReferenceSR``/``SGDMReferenceRN`` (sr_states/optim/sgd.py:19-69)
-take the reference's arguments, group keys and checkpoint layout and update
-one parameter at a time through the functional ``adamw_step_``/``sgdm_step_``,
-so each parameter costs one HIP launch.  Their bytes equal those of the fused
+take the reference's arguments, group keys and checkpoint layout.  The
+reference updates one parameter at a time through the functional
+``adamw_step_``/``sgdm_step_``; its bytes equal those of the fused
 multi-tensor ``AdamWHip``/``SGDMHip``, which update a whole group per launch.
-Unlike the fused optimizers they accept rounding rules registered with
-``register_rounding``: the moments are then updated in FP32 and stored
-through the registered routine.
+So a group runs as one fused launch per bucket whenever the fused launch
+takes it as it is, and one parameter at a time through the functional
+updates otherwise:
+
+- a state format without a HIP implementation (a rule registered with
+  ``register_rounding``: the moments are then updated in FP32 and stored
+  through the registered routine);
+- hyperparameters outside the fused optimizers' ranges (the reference's
+  eager updates compute with any);
+- a parameter, gradient or state the fused launch refuses (another dtype
+  than FP32/BF16, a strided layout, storage shared between parameters,
+  whose updates the reference applies in order);
+- a stream under HIP graph capture.
+
+The fused launch validates the whole group before it queues anything, so
+a refused group is updated per parameter from the start.
 """
 
 from __future__ import annotations
 
+import torch
+
+from ..hip._common import validate_update_device
+from ..hip._multi_tensor import prepare_group
+from ..hip._optimizer import DEFAULT_BLOCK_SIZE
+from ..hip.adamw import AdamWHip
+from ..hip.sgd import SGDMHip
 from ..reference.adamw import adamw_step_
 from ..reference.sgd import sgdm_step_
+from ..rounding import has_native
 from ._state import StateOptimizer
 from .adamw import validate_adamw
 from .sgd import validate_sgdm
 
 
-class AdamWReferenceSR(StateOptimizer):
+class _FusedGroups(StateOptimizer):
+    """Groups the fused multi-tensor launch takes as they are run on it; others per parameter."""
+
+    # Cleared on an instance, every group runs per parameter (the tests
+    # compare the two routes).
+    _fused_route = True
+
+    def _group_block_size(self, group):
+        return DEFAULT_BLOCK_SIZE
+
+    def _step_group(self, group, formats, items, rng_step):
+        prepared = self._fused_prepare(group, formats, items)
+        if prepared is not None:
+            self._launch_prepared(group, formats, prepared, rng_step)
+            return
+        first_index = 0
+        for other in self.param_groups:
+            if other is group:
+                break
+            first_index += len(other["params"])
+        # A fresh walk: the fused preparation may have consumed `items`.
+        super()._step_group(group, formats, self._group_items(group, formats, first_index), rng_step)
+
+    def _fused_prepare(self, group, formats, items):
+        """The fused launches of the group, or None to update it per parameter."""
+        if not self._fused_route or not all(has_native(f.dtype, f.rounding) for f in formats):
+            return None
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            return None
+        try:
+            self._validate_group(group)
+            # Validates every parameter, gradient and state of the group, and
+            # their disjointness, before anything is queued.
+            return prepare_group(self, group, formats, items, validate_update_device)
+        except (ValueError, TypeError):
+            return None
+
+
+class AdamWReferenceSR(_FusedGroups):
     """AdamW with FP32 arithmetic and a configurable format for each moment."""
 
     _state_names = ("exp_avg", "exp_avg_sq")
@@ -52,6 +111,8 @@ class AdamWReferenceSR(StateOptimizer):
     def _validate_group(self, group):
         validate_adamw(group)
 
+    _launch_prepared = AdamWHip._launch_prepared
+
     def _step_parameter(self, parameter, state, group, formats, step, seed, offset):
         local_p, local_g, exp_avg, exp_avg_sq = self._local_tensors(parameter, state)
         beta1, beta2 = group["betas"]
@@ -78,7 +139,7 @@ class AdamWReferenceRN(AdamWReferenceSR):
     _forced_rounding = "nearest"
 
 
-class SGDMReferenceSR(StateOptimizer):
+class SGDMReferenceSR(_FusedGroups):
     """Momentum SGD with FP32 arithmetic; BF16 stochastic storage by default."""
 
     _state_names = ("momentum_buffer",)
@@ -107,6 +168,8 @@ class SGDMReferenceSR(StateOptimizer):
 
     def _validate_group(self, group):
         validate_sgdm(group)
+
+    _launch_prepared = SGDMHip._launch_prepared
 
     def _step_parameter(self, parameter, state, group, formats, step, seed, offset):
         local_p, local_g, momentum = self._local_tensors(parameter, state)

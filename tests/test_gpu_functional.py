@@ -212,9 +212,11 @@ def _gradients(params, step):
         param.grad = None if i == 2 else (torch.randn(param.shape, generator=gen) * 0.1).to(param.device)
 
 
-def _run(optimizer_type, steps, device, **options):
+def _run(optimizer_type, steps, device, fused_route=True, **options):
     params = _model(device)
     optimizer = optimizer_type([{"params": params[:2]}, {"params": params[2:], "lr": 3e-3}], **options)
+    if not fused_route:
+        optimizer._fused_route = False
     for step in range(steps):
         _gradients(params, step)
         optimizer.step()
@@ -244,8 +246,11 @@ def _assert_same_run(a, b):
     (sr_states.SGDMReferenceRN, sr_states.SGDMHipRN, {"lr": 1e-2}),
 ], ids=["adamw_sr", "adamw_rn", "sgdm_sr", "sgdm_rn"])
 def test_per_parameter_optimizers_equal_the_fused_ones(cuda, eager, fused, options):
-    eager_run = _run(eager, 3, cuda, **options)
+    """The reference-named optimizers, one parameter at a time, equal the fused ones; so does
+    their own fused route."""
+    eager_run = _run(eager, 3, cuda, fused_route=False, **options)
     _assert_same_run(eager_run, _run(fused, 3, cuda, **options))
+    _assert_same_run(eager_run, _run(eager, 3, cuda, **options))
     # The checkpoint layout is shared: the fused optimizer resumes the eager one.
     params, optimizer = eager_run
     resumed_params = [torch.nn.Parameter(p.detach().clone()) for p in params]
@@ -368,3 +373,79 @@ def test_reference_sgdm_takes_any_hyperparameters_as_the_reference_does(cuda, hy
     _assert_all([got[0], got[2]], [want[0], want[2]], f"sgdm_step_ {hyper}")
     with pytest.raises(ValueError, match="invalid"):
         sr_states.hip_sgdm_step_(*got, formats=_fmts(formats), seed=KEY, offset=OFFSET, **options)
+
+
+def _route_counter(monkeypatch):
+    """Counts the groups the reference-named optimizers run on the fused launch."""
+    from sr_states.optim import eager as eager_module
+
+    counts = {"fused": 0}
+    original = eager_module._FusedGroups._fused_prepare
+
+    def counting(self, group, formats, items):
+        prepared = original(self, group, formats, items)
+        counts["fused"] += prepared is not None
+        return prepared
+
+    monkeypatch.setattr(eager_module._FusedGroups, "_fused_prepare", counting)
+    return counts
+
+
+@pytest.mark.parametrize("cls", [sr_states.AdamWReferenceSR, sr_states.SGDMReferenceSR], ids=lambda c: c.__name__)
+def test_reference_named_optimizers_fall_back_per_parameter_where_the_fused_launch_refuses(cuda, cls,
+                                                                                            monkeypatch):
+    """Groups the fused launch refuses update one parameter at a time, as before.
+
+    Each case runs both routes from the same start and compares every byte:
+    a strided parameter, two parameters sharing storage (updated in order,
+    the second reading what the first wrote) and a learning rate set below
+    zero after construction.  (Registered rules without a HIP kernel run per
+    parameter too: test_registered_rules_are_applied_by_the_functional_and_
+    eager_updates.)
+    """
+    counts = _route_counter(monkeypatch)
+    lr = 1e-2
+
+    def run(make_params, fused_route):
+        params = make_params()
+        optimizer = cls(params, lr=lr, seed=5)
+        optimizer._fused_route = fused_route
+        for step in range(3):
+            _gradients(params, step)
+            optimizer.step()
+        return params, optimizer
+
+    def plain():
+        return _model(cuda, seed=1)
+
+    def strided():
+        params = _model(cuda, seed=1)
+        gen = torch.Generator().manual_seed(3)
+        params[0] = torch.nn.Parameter(torch.randn(17, 33, generator=gen).to(cuda).t())
+        return params
+
+    def shared():
+        base = torch.randn(2000, generator=torch.Generator().manual_seed(4)).to(cuda)
+        return [torch.nn.Parameter(base[:1000]), torch.nn.Parameter(base[500:1500])]
+
+    counts["fused"] = 0
+    _assert_same_run(run(plain, True), run(plain, False))
+    assert counts["fused"] == 3  # three steps, one group, all on the fused launch
+    for make in (strided, shared):
+        counts["fused"] = 0
+        _assert_same_run(run(make, True), run(make, False))
+        assert counts["fused"] == 0, make.__name__
+    # A negative learning rate set after construction: the reference computes with it.
+    routes = []
+    for fused_route in (True, False):
+        params = _model(cuda, seed=2)
+        optimizer = cls(params, lr=lr, seed=5)
+        optimizer._fused_route = fused_route
+        optimizer.param_groups[0]["lr"] = -lr
+        counts["fused"] = 0
+        for step in range(2):
+            _gradients(params, step)
+            optimizer.step()
+        assert counts["fused"] == 0
+        routes.append((params, optimizer))
+    _assert_same_run(*routes)
