@@ -2,8 +2,9 @@
 
 The public surface follows the reference package ``sr_states``:
 ``StateFormat``, ``StateOptimizer``, ``cast``, ``register_rounding`` and the
-per-parameter optimizers ``AdamWReferenceSR/RN`` and ``SGDMReferenceSR/RN``
-at the top level, the functional updates in ``sr_states.reference``, and the
+optimizers ``AdamWReferenceSR/RN`` and ``SGDMReferenceSR/RN`` (the fused
+launch for the groups it takes, one parameter at a time otherwise) at the
+top level, the functional updates in ``sr_states.reference``, and the
 fused multi-tensor optimizers and casts in ``sr_states.hip`` (the
 counterpart of ``sr_states.triton``).  All arithmetic runs in the HIP
 library ``libsr_states_hip.so``; there is no CPU execution path.

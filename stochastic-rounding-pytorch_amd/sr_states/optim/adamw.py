@@ -39,7 +39,7 @@ def adamw_hparams(lr, beta1, beta2, eps, weight_decay, step) -> _lib.AdamWHparam
 
 
 def __getattr__(name):
-    """``AdamWReferenceSR``/``AdamWReferenceRN``, defined with the other per-parameter optimizers."""
+    """``AdamWReferenceSR``/``AdamWReferenceRN``, defined with the other reference-named optimizers."""
     if name in ("AdamWReferenceSR", "AdamWReferenceRN"):
         from . import eager
 

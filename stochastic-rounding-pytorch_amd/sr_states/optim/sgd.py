@@ -26,7 +26,7 @@ def sgdm_hparams(lr, momentum) -> _lib.SgdmHparams:
 
 
 def __getattr__(name):
-    """``SGDMReferenceSR``/``SGDMReferenceRN``, defined with the other per-parameter optimizers."""
+    """``SGDMReferenceSR``/``SGDMReferenceRN``, defined with the other reference-named optimizers."""
     if name in ("SGDMReferenceSR", "SGDMReferenceRN"):
         from . import eager
 

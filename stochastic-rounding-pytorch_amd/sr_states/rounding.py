@@ -40,7 +40,8 @@ def register_rounding(
     Names and dtypes are stored in checkpoints; callables are not.  Replacing a
     registration is forbidden.  Rules registered here have no HIP
     implementation, so fused HIP optimizers reject them; ``cast`` and the
-    per-parameter optimizers apply ``reference``.
+    reference-named optimizers (one parameter at a time for such groups)
+    apply ``reference``.
 
     ``triton`` is the reference's optional Triton callback for its fused
     kernels.  It is accepted so that registrations written for the reference
