@@ -1,4 +1,4 @@
-"""Per-parameter optimizers under the reference's eager names.
+"""Optimizers under the reference's eager names: fused groups, or one parameter at a time.
 
 ``AdamWReferenceSR``/``AdamWReferenceRN`` (sr_states/optim/adamw.py:21-79)
 and ``SGDMReferenceSR``/``SGDMReferenceRN`` (sr_states/optim/sgd.py:19-69)
