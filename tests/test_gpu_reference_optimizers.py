@@ -1,4 +1,5 @@
-"""The per-parameter optimizers under the reference's names, on the GPU.
+"""The optimizers under the reference's names, on the GPU (their fused route:
+every group here is one the fused launch takes).
 
 Mirrors tests/test_reference_optimizers.py:1-103 of the reference (FP32
 states against torch.optim, BF16 state bytes, the RNG position carried by a
