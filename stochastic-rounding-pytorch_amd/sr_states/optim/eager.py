@@ -18,10 +18,15 @@ updates otherwise:
 - a parameter, gradient or state the fused launch refuses (another dtype
   than FP32/BF16, a strided layout, storage shared between parameters,
   whose updates the reference applies in order);
-- a stream under HIP graph capture.
+- a stream under HIP graph capture;
+- a parameter the reference's walk raises at (a sparse gradient, a DTensor
+  placement without a flat shard start, more than 2**32 elements).
 
 The fused launch validates the whole group before it queues anything, so
-a refused group is updated per parameter from the start.
+a refused group is updated per parameter from the start.  For the last
+kind, that walk updates every parameter ahead of the bad one and records
+its step before it raises the same error at the same parameter, as the
+reference's lazy loop does (sr_states/optim/_state.py:154-182).
 """
 
 from __future__ import annotations
@@ -75,7 +80,11 @@ class _FusedGroups(StateOptimizer):
             # Validates every parameter, gradient and state of the group, and
             # their disjointness, before anything is queued.
             return prepare_group(self, group, formats, items, validate_update_device)
-        except (ValueError, TypeError):
+        except (ValueError, TypeError, RuntimeError):
+            # RuntimeError covers the walk's sparse-gradient refusal and
+            # NotImplementedError (unsupported DTensor placements): the
+            # per-parameter route updates the parameters ahead of the bad one
+            # before raising it again.
             return None
 
 
