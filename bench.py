@@ -30,8 +30,14 @@ present.
 the same streams (widths, tile shape and order, non-temporal accesses) over
 the same number of elements (tests/native/stream_ceiling.hip), timed in the
 same process after the workload's tensors are freed, also over
-back-to-back launches: what the memory system gives this access pattern at
-this footprint.  ``frac`` there is the fused kernel's rate over it.
+back-to-back launches, at the best of four stream placements and three
+resident-workgroup caps (none, the library's, half of it): what the memory
+system gives this access pattern at this footprint.  ``frac`` there is the
+fused kernel's rate over it.
+
+``--workload footprint_sweep`` times the fused AdamW kernel and the trivial
+kernel with the north star's streams on one tensor at six footprints from
+1.34 to 31 GB, each with the library's resident-workgroup cap and without.
 
 ``torch_fused``: torch's own ``torch.optim.AdamW`` / ``SGD`` with
 ``fused=True`` (states in the parameters' dtype), timed the same way on the same parameters
@@ -51,10 +57,6 @@ and compared byte for byte; the run fails if any byte differs.
 ``--workload cast_sizes`` times the reference cast benchmark's size sweep
 (2^10 to 2^24): this backend's stochastic and nearest BF16 casts and torch's
 conversion, per size.
-
-``--workload bandwidth_matrix`` instead times trivial-math kernels that move
-subsets and rearrangements of the north star's streams at its footprint
-(tests/native/bandwidth_matrix.hip) and prints their rates.
 """
 
 from __future__ import annotations
@@ -239,19 +241,22 @@ WORKLOADS = {
         hparams={},
         seed=0,
     ),
-    # Trivial-math stream variants at the north star's footprint
-    # (tests/native/bandwidth_matrix.hip): not an optimizer step.
-    "bandwidth_matrix": dict(
-        optimizer="matrix",
-        shapes=C4_BLOCK * 7 + [(32000, 4096)],
+    # The north star's streams (FP32 p/g, BF16-SR m/v) on one tensor at six
+    # footprints from 1.34 to 31 GB: the fused kernel and the trivial kernel
+    # with the same streams, each with the library's resident-workgroup cap
+    # and without one (tests/native/stream_ceiling.hip, sr_launch_cap_sweep).
+    # steps = launches per measurement, warmup = interleaved rounds.
+    "footprint_sweep": dict(
+        optimizer="footprint",
+        shapes=[(1547698176,)],
         p_dtype=torch.float32,
         g_dtype=torch.float32,
         formats=((torch.bfloat16, "stochastic"), (torch.bfloat16, "stochastic")),
-        grad_std=1.0,
+        grad_std=1e-3,
         hparams={},
         seed=0,
-        steps=10,
-        warmup=3,
+        steps=100,
+        warmup=2,
     ),
     # The reference cast benchmark's size sweep (benchmarks/bench_sr_cast.py:
     # 25-27: 2^10 to 2^24 in steps of 4x) of FP32 -> BF16: this backend's
@@ -822,67 +827,39 @@ def pattern_ceiling(spec, elements: int, reps: int):
             "elements": n, "kernel": "stream_ceiling.hip: same streams, trivial arithmetic"}
 
 
-MATRIX_LIBRARY = ROOT / "tests" / "native" / "libbandwidth_matrix.so"
+FOOTPRINTS_GB = (1.34, 2.68, 5.0, 10.0, 20.0, 30.95)
 
 
-def bandwidth_matrix(elements: int, reps: int, rounds: int):
-    """Rates of every variant of tests/native/bandwidth_matrix.hip over `elements` elements."""
-    import ctypes
-
-    if not MATRIX_LIBRARY.exists():
-        raise SystemExit(f"{MATRIX_LIBRARY} is not built (tests/native/build_checks.py)")
-    lib = ctypes.CDLL(str(MATRIX_LIBRARY))
-    lib.sr_bandwidth_variants.restype = ctypes.c_int
-    lib.sr_bandwidth_variant.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int)]
-    lib.sr_bandwidth_matrix.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
-                                        ctypes.POINTER(ctypes.c_float), ctypes.c_int]
-    count = lib.sr_bandwidth_variants()
-    ms = (ctypes.c_float * (count * rounds))()
-    n = elements // 4096 * 4096
-    if lib.sr_bandwidth_matrix(n, reps, rounds, ms, count) != 0:
-        raise SystemExit("sr_bandwidth_matrix failed")
-    rows = []
-    for v in range(count):
-        name, width = ctypes.c_char_p(), ctypes.c_int()
-        lib.sr_bandwidth_variant(v, ctypes.byref(name), ctypes.byref(width))
-        times = [ms[r * count + v] for r in range(rounds)]
-        rows.append({"variant": name.value.decode(), "bytes_per_element": width.value,
-                     "best_gbps": width.value * n / min(times) / 1e6,
-                     "mean_gbps": width.value * n / statistics.mean(times) / 1e6,
-                     "ms": times})
-    return n, rows
-
-
-# Gaps between consecutive stream bases for the placement sweep.
-PLACEMENT_GAPS = (0, 256, 4096, 65536, 1 << 20, 2 << 20, (2 << 20) + 4096, 3 << 20, 16 << 20)
-
-
-def stream_placements(elements: int, reps: int):
-    """Rate of the trivial kernel with the fused update's streams at several stream placements.
-
-    For the north star's streams (FP32 p/g, BF16 m/v) and the same with BF16
-    p/g: one allocation, each stream PLACEMENT_GAPS[i] bytes after the end of
-    the previous one (tests/native/stream_ceiling.hip, sr_stream_placements).
-    """
+def footprint_sweep(reps: int, rounds: int):
+    """Rates of the fused AdamW kernel and the trivial kernel by footprint, with and without the cap."""
     import ctypes
 
     if not CEILING_LIBRARY.exists():
         raise SystemExit(f"{CEILING_LIBRARY} is not built (tests/native/build_checks.py)")
     lib = ctypes.CDLL(str(CEILING_LIBRARY))
-    lib.sr_stream_placements.restype = ctypes.c_int
-    lib.sr_stream_placements.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                         ctypes.c_int, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int,
-                                         ctypes.POINTER(ctypes.c_float)]
-    n = elements // 512 * 512
-    gaps = (ctypes.c_uint64 * len(PLACEMENT_GAPS))(*PLACEMENT_GAPS)
-    out = []
-    for name, widths, bpe in (("fp32_params", (4, 4, 2, 2), 20), ("bf16_params", (2, 2, 2, 2), 14)):
-        ms = (ctypes.c_float * len(PLACEMENT_GAPS))()
-        if lib.sr_stream_placements(n, *widths, reps, gaps, len(PLACEMENT_GAPS), ms) != 0:
-            raise SystemExit("sr_stream_placements failed")
-        out.append({"streams": name, "bytes_per_element": bpe,
-                    "gbps_by_gap": {str(g): bpe * n / t / 1e6 for g, t in zip(PLACEMENT_GAPS, ms)}})
-    return out
+    lib.sr_launch_cap_sweep.restype = ctypes.c_int
+    lib.sr_launch_cap_sweep.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.POINTER(ctypes.c_int), ctypes.c_int,
+                                        ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float),
+                                        ctypes.POINTER(ctypes.c_int)]
+    caps = (ctypes.c_int * 2)(-1, 0)  # the library's rule, then none
+    rows = []
+    for _ in range(rounds):
+        for gb in FOOTPRINTS_GB:
+            n = int(gb * 1e9 / 20) >> 21 << 21  # whole 2^21-element chunk rounds
+            trivial, fused, resident = (ctypes.c_float * 2)(), (ctypes.c_float * 2)(), (ctypes.c_int * 2)()
+            if lib.sr_launch_cap_sweep(n, max(5, min(reps, int(300 / (n * 20 / 6e9)))), caps, 2, trivial, fused,
+                                       resident) != 0:
+                raise SystemExit("sr_launch_cap_sweep failed")
+            rate = lambda ms: 20 * n / ms / 1e6  # noqa: E731  (GB/s)
+            rows.append({"elements": n, "gb": 20 * n / 1e9,
+                         "fused_capped_gbps": rate(fused[0]), "fused_uncapped_gbps": rate(fused[1]),
+                         "trivial_capped_gbps": rate(trivial[0]), "trivial_uncapped_gbps": rate(trivial[1]),
+                         "resident_capped": resident[0], "resident_uncapped": resident[1]})
+            print(f"footprint {rows[-1]['gb']:.2f} GB: fused {rows[-1]['fused_capped_gbps']:.0f} / "
+                  f"{rows[-1]['fused_uncapped_gbps']:.0f} GB/s (cap {resident[0]} / {resident[1]} per CU), trivial "
+                  f"{rows[-1]['trivial_capped_gbps']:.0f} / {rows[-1]['trivial_uncapped_gbps']:.0f}",
+                  file=sys.stderr, flush=True)
+    return rows
 
 
 def load_traffic(workload: str):
@@ -964,18 +941,19 @@ def main():
     if args.steps is None:
         args.steps = spec.get("steps", 100)
     device = torch.device("cuda", 0)
-    if spec["optimizer"] == "matrix":
+    if spec["optimizer"] == "footprint":
         if args.warmup < 1:
-            raise SystemExit("--workload bandwidth_matrix takes --warmup as its number of rounds: at least 1")
-        n, rows = bandwidth_matrix(sum(math.prod(s) for s in spec["shapes"]), args.steps, args.warmup)
-        placements = stream_placements(sum(math.prod(s) for s in spec["shapes"]), args.steps)
+            raise SystemExit("--workload footprint_sweep takes --warmup as its number of rounds: at least 1")
+        rows = footprint_sweep(args.steps, args.warmup)
         print(json.dumps({
-            "metric": "bandwidth of trivial-math stream variants at the north star's footprint, 1 MI355X",
-            "value": rows[0]["best_gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "higher_is_better": True, "vs_baseline": None, "dtype": "u32",
-            "data": "constant fill, XOR folds", "elements": n,
-            "note": "steps = launches per variant per round, warmup = interleaved rounds",
-            "peak": HBM_PEAK_GBPS, "matrix": rows, "placements": placements}), flush=True)
+            "metric": "fused AdamW and trivial-kernel rates by footprint, with and without the resident cap, "
+                      "1 MI355X",
+            "value": rows[-1]["fused_capped_gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "higher_is_better": True, "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (hashed uniform draws on the GPU)",
+            "note": "steps = launches per measurement (fewer for large footprints), warmup = interleaved rounds; "
+                    "value = the fused kernel, capped, at the largest footprint",
+            "peak": HBM_PEAK_GBPS, "rows": rows}), flush=True)
         return
     if spec["optimizer"] == "cast_sweep":
         rows = cast_sizes(spec, args.steps, args.warmup)

@@ -13,6 +13,7 @@
 
 #include "../../include/sr_states_hip.h"
 #include "sr_kernels.h"
+#include "sr_launch_cap.h"
 
 namespace {
 
@@ -84,15 +85,33 @@ bool valid_block(int block) { return block >= 64 && block <= sr::kMaxBlock && bl
 // rounds so that the kernels' tile order (sr_tile_order.h) is a permutation,
 // and split into rows when one dimension would carry 2^32 or more
 // work-items (2^34 elements at four per lane).  `tiles` must equal the
-// total_tiles the kernel argument carries.
-int launch(const void* fn, int block, uint32_t tiles, void* arg, void* stream) {
+// total_tiles the kernel argument carries.  `cap` > 0 limits the resident
+// workgroups per CU to that many (sr::cap_lds).
+int launch(const void* fn, int block, uint32_t tiles, void* arg, void* stream, uint32_t cap = 0) {
   if (sr::padded_grid(tiles) > 0x7FFFFFFFull) return fail(SR_ERR_ARGUMENT, "%u tiles exceed the grid limit", tiles);
   const sr::LaunchShape shape = sr::launch_shape(tiles, static_cast<uint32_t>(block));
   void* args[] = {arg};
-  hipError_t err = hipLaunchKernel(fn, dim3(shape.x, shape.y), dim3(block), args, 0,
+  hipError_t err = hipLaunchKernel(fn, dim3(shape.x, shape.y), dim3(block), args, sr::cap_lds(fn, block, cap),
                                    static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return hip_fail(err, "hipLaunchKernel");
   return SR_OK;
+}
+
+// Resident-workgroup cap of an AdamW launch (sr::resident_cap).
+uint32_t adamw_cap(int pi, int gi, int me, int ve, int block, uint32_t tiles) {
+  const int bytes = 2 * sr::enc_bytes(param_enc(pi)) + sr::enc_bytes(param_enc(gi)) + 2 * sr::enc_bytes(me) +
+                    2 * sr::enc_bytes(ve);
+  return sr::resident_cap(tiles, static_cast<uint32_t>(block),
+                          static_cast<uint32_t>(sr::lane_elements(param_enc(pi), param_enc(gi), me, ve)),
+                          static_cast<uint32_t>(bytes), pi == 0);
+}
+
+// Resident-workgroup cap of a momentum-SGD launch.
+uint32_t sgdm_cap(int pi, int gi, int ue, int block, uint32_t tiles) {
+  const int bytes = 2 * sr::enc_bytes(param_enc(pi)) + sr::enc_bytes(param_enc(gi)) + 2 * sr::enc_bytes(ue);
+  return sr::resident_cap(tiles, static_cast<uint32_t>(block),
+                          static_cast<uint32_t>(sr::lane_elements(param_enc(pi), param_enc(gi), ue, ue)),
+                          static_cast<uint32_t>(bytes), pi == 0);
 }
 
 // Tiles of block * lanes elements covering n elements, or fail if they do
@@ -304,7 +323,8 @@ int sr_adamw_step(void* p, const void* g, void* m, void* v, int64_t n, int p_dty
   r.shard_start = offset;
   r.flags = SR_ROW_KEYED |
             ((aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v)) ? SR_ROW_VECTOR : 0u);
-  return launch(tables().adamw[pi][gi][me][ve], block_size, a.total_tiles, &a, stream);
+  return launch(tables().adamw[pi][gi][me][ve], block_size, a.total_tiles, &a, stream,
+                adamw_cap(pi, gi, me, ve, block_size, a.total_tiles));
 }
 
 int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, const float* row_scalars,
@@ -331,7 +351,8 @@ int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, const float* r
   a.key_prefix = sr::update_key_prefix(static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32),
                                        static_cast<uint32_t>(rng_step),
                                        static_cast<uint32_t>(rng_step >> 32));
-  return launch(tables().adamw[pi][gi][me][ve], block_size, total_tiles, &a, stream);
+  return launch(tables().adamw[pi][gi][me][ve], block_size, total_tiles, &a, stream,
+                adamw_cap(pi, gi, me, ve, block_size, total_tiles));
 }
 
 int sr_sgdm_step(void* p, const void* g, void* u, int64_t n, int p_dtype, int g_dtype, int u_dtype,
@@ -363,7 +384,8 @@ int sr_sgdm_step(void* p, const void* g, void* u, int64_t n, int p_dtype, int g_
   r.param_index = key;
   r.shard_start = offset;
   r.flags = SR_ROW_KEYED | ((aligned16(p) && aligned16(g) && aligned16(u)) ? SR_ROW_VECTOR : 0u);
-  return launch(tables().sgdm[pi][gi][ue], block_size, a.total_tiles, &a, stream);
+  return launch(tables().sgdm[pi][gi][ue], block_size, a.total_tiles, &a, stream,
+                sgdm_cap(pi, gi, ue, block_size, a.total_tiles));
 }
 
 int sr_sgdm_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint32_t total_tiles,
@@ -386,7 +408,8 @@ int sr_sgdm_multi(const sr_row* rows, const uint32_t* tile_rows, int nrows, uint
   a.key_prefix = sr::update_key_prefix(static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32),
                                        static_cast<uint32_t>(rng_step),
                                        static_cast<uint32_t>(rng_step >> 32));
-  return launch(tables().sgdm[pi][gi][ue], block_size, total_tiles, &a, stream);
+  return launch(tables().sgdm[pi][gi][ue], block_size, total_tiles, &a, stream,
+                sgdm_cap(pi, gi, ue, block_size, total_tiles));
 }
 
 int sr_adamw_multi_noalloc(const sr_row* rows, const float* row_scalars, int nrows, uint32_t total_tiles,
@@ -436,7 +459,8 @@ int sr_adamw_multi_noalloc(const sr_row* rows, const float* row_scalars, int nro
   a.key_prefix = sr::update_key_prefix(static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32),
                                        static_cast<uint32_t>(rng_step),
                                        static_cast<uint32_t>(rng_step >> 32));
-  return launch(tables().adamw[pi][gi][me][ve], block_size, total_tiles, &a, stream);
+  return launch(tables().adamw[pi][gi][me][ve], block_size, total_tiles, &a, stream,
+                adamw_cap(pi, gi, me, ve, block_size, total_tiles));
 }
 
 }  // extern "C"

@@ -1,7 +1,9 @@
 // sr_tile_order.h -- which tile each workgroup of a launch processes.
 //
 // Shared by the kernels and by the host code that sizes the grid, and plain
-// C++ otherwise, so it also compiles on the host alone.
+// C++ otherwise, so it also compiles on the host alone.  It also holds the
+// rule for how many workgroups of a large optimizer launch stay resident
+// per CU (resident_cap, at the end).
 //
 // The dispatcher hands workgroup b to XCD (b mod 8).  Tiles are dealt to the
 // XCDs in chunks of 2^s consecutive tiles: XCD x takes chunks x, x + 8,
@@ -71,6 +73,38 @@ SR_HOST_DEVICE inline LaunchShape launch_shape(uint32_t tiles, uint32_t block,
   uint64_t per_row = max_items / block / unit * unit;
   if (per_row == 0) per_row = unit;  // only for limits below one chunk round
   return {static_cast<uint32_t>(per_row), static_cast<uint32_t>((grid + per_row - 1) / per_row)};
+}
+
+// Resident workgroups per CU of a large optimizer launch.  The fused updates
+// use few registers, so 16 of their 128-lane workgroups fit on a CU, and
+// that many keep more memory requests in flight than HBM can serve: the
+// surplus only adds contention.  Measured on MI355X (every cap exact,
+// interleaved in one process), the rate peaks with about 80 KiB of tiles
+// in flight per CU, i.e. cap = round(80 KiB / tile bytes):
+//   north star (FP32 p/g, BF16-SR m/v, 20 B):  6.04 -> 6.46 TB/s at 8
+//   2^26-element tensor, same streams:           6.45 -> 6.71 at 8
+//   E4M3 m + BF16 v (18 B): 6.17 -> 6.41 at 9;  BF16 g (18 B): 6.33 -> 6.61 at 9
+//   SGDM, FP16 momentum (16 B): 6.37 -> 6.61 at 8 (6.49 at the rule's 10)
+//   FP32 moments (28 B): 5.91 -> 6.47 at 5 (6.31 at the rule's 6)
+// Launches with BF16 parameters spend more of a workgroup's life in
+// arithmetic; caps of 11 to 15 moved them by under 1%, so they stay
+// uncapped, as do launches of fewer than 2^16 tiles (2^25 elements at 128
+// lanes), whose tail the cap lengthens (2^24 elements: 6.50 -> 6.46;
+// 2^25: 6.53 -> 6.62), and the casts (every cap slower).
+constexpr uint32_t kInFlightBytesPerCu = 80u * 1024u;
+constexpr uint32_t kResidentCapMinTiles = 1u << 16;
+constexpr uint32_t kResidentCapMax = 12;
+
+// Workgroups per CU to leave resident for an optimizer launch of `tiles`
+// tiles of `block` lanes times `lanes` elements, moving `bytes_per_element`
+// bytes per element, or 0 for no cap.
+SR_HOST_DEVICE inline uint32_t resident_cap(uint32_t tiles, uint32_t block, uint32_t lanes,
+                                            uint32_t bytes_per_element, bool fp32_params) {
+  if (!fp32_params || tiles < kResidentCapMinTiles) return 0;
+  const uint64_t tile_bytes = static_cast<uint64_t>(block) * lanes * bytes_per_element;
+  if (tile_bytes == 0) return 0;
+  const uint64_t cap = (kInFlightBytesPerCu + tile_bytes / 2) / tile_bytes;
+  return cap >= 1 && cap <= kResidentCapMax ? static_cast<uint32_t>(cap) : 0u;
 }
 
 }  // namespace sr

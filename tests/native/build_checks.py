@@ -12,9 +12,7 @@
   checks it against the C oracle (when the package library is built);
 - tests/native/libstream_ceiling.so, the trivial-math kernel of
   stream_ceiling.hip that measures the bandwidth ceiling of the fused
-  update's access pattern (bench.py and tests/test_gpu_stream_ceiling.py);
-- tests/native/libbandwidth_matrix.so, the trivial-math stream variants of
-  bandwidth_matrix.hip (bench.py --workload bandwidth_matrix).
+  update's access pattern (bench.py and tests/test_gpu_stream_ceiling.py).
 
 __graft_entry__.build() calls it; tests/conftest.py calls it on a CPU
 checkout where a library is missing.  GPU runs use the prebuilt files.
@@ -33,10 +31,8 @@ CHECK_LIBRARY = HERE / "libbf16_sr_check.so"
 CEILING_LIBRARY = HERE / "libstream_ceiling.so"
 MINIFLOAT_LIBRARY = HERE / "libminifloat_check.so"
 DIVSQRT_LIBRARY = HERE / "libdivsqrt_check.so"
-MATRIX_LIBRARY = HERE / "libbandwidth_matrix.so"
 LIBRARIES = {CHECK_LIBRARY: HERE / "bf16_sr_check.hip", CEILING_LIBRARY: HERE / "stream_ceiling.hip",
-             MINIFLOAT_LIBRARY: HERE / "minifloat_check.hip", DIVSQRT_LIBRARY: HERE / "divsqrt_check.hip",
-             MATRIX_LIBRARY: HERE / "bandwidth_matrix.hip"}
+             MINIFLOAT_LIBRARY: HERE / "minifloat_check.hip", DIVSQRT_LIBRARY: HERE / "divsqrt_check.hip"}
 
 
 def _package_build():

@@ -1,18 +1,24 @@
 // The bandwidth ceiling of a fused update's access pattern, measured.
 //
-// A kernel with trivial arithmetic (XORs) that moves exactly the
-// streams of one fused-update launch: a parameter (FP32 or BF16) read and
-// written, a gradient read, and one or two states read and written, with the product's
+// A kernel with trivial arithmetic (XORs) that moves exactly the streams of
+// one fused-update launch: a parameter (FP32 or BF16) read and written, a
+// gradient read, and one or two states read and written, with the product's
 // tile shape (128 lanes x 4 elements), its XCD-chunked tile order
 // (sr_tile_order.h), its addressing (a scalar tile base plus a 32-bit lane
-// offset) and its non-temporal accesses.  Whatever rate this
-// kernel reaches for n elements is what the memory system gives that access
-// pattern at that footprint; the fused kernels do strictly more work per
-// byte, so their rate over this one says how much of the reachable
-// bandwidth their arithmetic and table lookups cost.
+// offset), its non-temporal accesses and its resident-workgroup cap
+// (sr::resident_cap, enforced with sr::cap_lds as the library's launches
+// do).  Whatever rate this kernel reaches for n elements is what the memory
+// system gives that access pattern at that footprint; the fused kernels do
+// strictly more work per byte, so their rate over this one says how much of
+// the reachable bandwidth their arithmetic and table lookups cost.
 //
 // sr_cast_ceiling does the same for the cast's pattern (FP32 in, a 2- or
 // 1-byte format out) with the cast's launch shape.
+//
+// sr_launch_cap_sweep times this kernel beside the library's own fused AdamW
+// kernel (FP32 parameter and gradient, BF16 stochastic moments: the north
+// star's instantiation, on one tensor) at caller-chosen resident-workgroup
+// caps, to show what the cap rule gains at a given footprint.
 //
 // Measurement helper only: bench.py reports it beside the fused kernel's
 // rate and tests/test_gpu_stream_ceiling.py checks the fused kernels against
@@ -21,6 +27,8 @@
 
 #include <cstdint>
 
+#include "../../stochastic-rounding-pytorch_amd/csrc/sr_kernels.h"
+#include "../../stochastic-rounding-pytorch_amd/csrc/sr_launch_cap.h"
 #include "../../stochastic-rounding-pytorch_amd/csrc/sr_tile_order.h"
 
 namespace {
@@ -138,8 +146,8 @@ Kernel pick(int p, int g, int m, int v) {
 
 // The placements the ceiling tries: gaps between consecutive stream bases in
 // one allocation.  Where the streams land relative to each other moves the
-// rate of this pattern by a few percent (bench.py --workload
-// bandwidth_matrix prints a sweep), so the ceiling is the best of several.
+// rate of this pattern by a few percent, so the ceiling is the best of
+// several.
 constexpr uint64_t kCeilingGaps[] = {0, 4096, 65536, 16ull << 20};
 constexpr uint64_t kMaxGap = 16ull << 20;
 
@@ -149,7 +157,7 @@ constexpr uint64_t kMaxGap = 16ull << 20;
 // per launch over `reps` launches after two untimed ones, or a negative
 // value on a HIP error.
 float time_placement(Kernel kernel, char* slab, const uint64_t (&bytes)[4], uint64_t gap, uint32_t tiles, int reps,
-                     hipEvent_t start, hipEvent_t stop) {
+                     size_t lds, hipEvent_t start, hipEvent_t stop) {
   void* bases[4] = {nullptr, nullptr, nullptr, nullptr};
   uint64_t at = 0;
   for (int k = 0; k < 4; ++k) {
@@ -159,7 +167,7 @@ float time_placement(Kernel kernel, char* slab, const uint64_t (&bytes)[4], uint
   }
   const sr::LaunchShape shape = sr::launch_shape(tiles, kBlock);
   auto launch = [&] {
-    hipLaunchKernelGGL(kernel, dim3(shape.x, shape.y), dim3(kBlock), 0, nullptr, bases[0], bases[1], bases[2],
+    hipLaunchKernelGGL(kernel, dim3(shape.x, shape.y), dim3(kBlock), lds, nullptr, bases[0], bases[1], bases[2],
                        bases[3], tiles);
   };
   launch();
@@ -174,10 +182,11 @@ float time_placement(Kernel kernel, char* slab, const uint64_t (&bytes)[4], uint
 }
 
 // Times `kernel` over n elements at each gap in gaps[0..count) (every gap at
-// most kMaxGap), writing milliseconds per launch to ms[0..count).  Returns 0,
-// or 2 for a HIP error (buffers are freed either way).
-int time_placements(Kernel kernel, uint64_t n, const int (&widths)[4], const uint64_t* gaps, int count, int reps,
-                    float* ms) {
+// most kMaxGap) and each resident-workgroup cap in caps[0..ncaps) (0: none),
+// writing milliseconds per launch to ms[cap_index * count + gap_index].
+// Returns 0, or 2 for a HIP error (buffers are freed either way).
+int time_placements(Kernel kernel, uint64_t n, const int (&widths)[4], const uint64_t* gaps, int count,
+                    const uint32_t* caps, int ncaps, int reps, float* ms) {
   const uint32_t tiles = static_cast<uint32_t>(n / kTile);
   const uint64_t bytes[4] = {n * widths[0], n * widths[1], n * widths[2], n * widths[3]};
   uint64_t total = 0;
@@ -192,9 +201,13 @@ int time_placements(Kernel kernel, uint64_t n, const int (&widths)[4], const uin
       break;
     if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess) break;
     bool failed = false;
-    for (int i = 0; i < count && !failed; ++i) {
-      ms[i] = time_placement(kernel, slab, bytes, gaps[i], tiles, reps, start, stop);
-      failed = ms[i] < 0.0f;
+    for (int c = 0; c < ncaps && !failed; ++c) {
+      const size_t lds = sr::cap_lds(reinterpret_cast<const void*>(kernel), kBlock, caps[c]);
+      for (int i = 0; i < count && !failed; ++i) {
+        float& out = ms[c * count + i];
+        out = time_placement(kernel, slab, bytes, gaps[i], tiles, reps, lds, start, stop);
+        failed = out < 0.0f;
+      }
     }
     if (!failed) rc = 0;
   } while (false);
@@ -207,12 +220,28 @@ int time_placements(Kernel kernel, uint64_t n, const int (&widths)[4], const uin
 
 bool valid_streams(uint64_t n, int reps) { return n != 0 && n % kTile == 0 && n / kTile <= 0x7FFFF000ull && reps >= 1; }
 
+// Parameters ~ U(-0.02, 0.02) and gradients ~ U(-1e-3, 1e-3) from a hash of
+// the index: finite values that keep the fused update on its common path.
+__global__ void fill_update_inputs(float* p, float* g, uint64_t n) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint32_t h = sr::h32(static_cast<uint32_t>(i) ^ 0x5EEDu), k = sr::h32(h ^ 0x9E3779B9u);
+    p[i] = ((h >> 8) * 0x1p-24f - 0.5f) * 0.04f;
+    g[i] = ((k >> 8) * 0x1p-24f - 0.5f) * 2e-3f;
+  }
+}
+
 }  // namespace
 
 // Average milliseconds per launch of the trivial kernel over n elements with
 // a parameter of p_bytes, a gradient of g_bytes and states of m_bytes and
 // v_bytes per element (v_bytes 0: one state), over `reps` launches after two
-// untimed ones, at the best of the placements kCeilingGaps.  Supported
+// untimed ones, at the best of the placements kCeilingGaps and of three
+// launch policies: no resident-workgroup cap, the library's cap for this
+// pattern (sr::resident_cap) and half of it.  (With no arithmetic to wait
+// for, the trivial kernel's workgroups are short-lived and it keeps enough
+// bytes in flight with fewer of them: the north star's streams at 31 GB ran
+// at 6.18 TB/s uncapped, 6.31 at 8 per CU and 6.38 at 4.)  Supported
 // (p, g, m, v) patterns: FP32 parameters with (4,2,2), (2,2,2), (4,1,2),
 // (4,2,0), (4,4,4), (4,1,1), (4,4,0), (4,1,0); BF16 parameters with (2,2,2),
 // (2,1,2), (2,2,0).  n must be a positive multiple of 512 with n / 512 <=
@@ -223,26 +252,20 @@ extern "C" int sr_stream_ceiling_p(uint64_t n, int p_bytes, int g_bytes, int m_b
                                    float* avg_ms) {
   const Kernel kernel = pick(p_bytes, g_bytes, m_bytes, v_bytes);
   if (!kernel || !valid_streams(n, reps) || !avg_ms) return 1;
+  const uint32_t per_element = 2 * p_bytes + g_bytes + 2 * m_bytes + 2 * v_bytes;
+  const uint32_t rule =
+      sr::resident_cap(static_cast<uint32_t>(n / kTile), kBlock, kLanes, per_element, p_bytes == 4);
+  uint32_t caps[3] = {0, rule, rule / 2};
+  const int ncaps = rule == 0 ? 1 : (rule / 2 == 0 ? 2 : 3);
   constexpr int kCount = sizeof(kCeilingGaps) / sizeof(kCeilingGaps[0]);
-  float ms[kCount];
-  const int rc = time_placements(kernel, n, {p_bytes, g_bytes, m_bytes, v_bytes}, kCeilingGaps, kCount, reps, ms);
+  float ms[3 * kCount];
+  const int rc = time_placements(kernel, n, {p_bytes, g_bytes, m_bytes, v_bytes}, kCeilingGaps, kCount, caps, ncaps,
+                                 reps, ms);
   if (rc != 0) return rc;
   float best = ms[0];
-  for (float t : ms) best = t < best ? t : best;
+  for (int i = 0; i < ncaps * kCount; ++i) best = ms[i] < best ? ms[i] : best;
   *avg_ms = best;
   return 0;
-}
-
-// The same kernel at caller-chosen placements: ms[i] receives the
-// milliseconds per launch with gaps[i] bytes (a multiple of 256, at most
-// 16 MiB) between consecutive stream bases; 1 <= count <= 64.
-extern "C" int sr_stream_placements(uint64_t n, int p_bytes, int g_bytes, int m_bytes, int v_bytes, int reps,
-                                    const uint64_t* gaps, int count, float* ms) {
-  const Kernel kernel = pick(p_bytes, g_bytes, m_bytes, v_bytes);
-  if (!kernel || !valid_streams(n, reps) || !gaps || !ms || count < 1 || count > 64) return 1;
-  for (int i = 0; i < count; ++i)
-    if (gaps[i] % 256 || gaps[i] > kMaxGap) return 1;
-  return time_placements(kernel, n, {p_bytes, g_bytes, m_bytes, v_bytes}, gaps, count, reps, ms);
 }
 
 // sr_stream_ceiling_p with an FP32 parameter.
@@ -300,5 +323,89 @@ extern "C" int sr_cast_ceiling(uint64_t n, int out_bytes, int buffers, int reps,
     if (in[k]) (void)hipFree(in[k]);
     if (out[k]) (void)hipFree(out[k]);
   }
+  return rc;
+}
+
+// Milliseconds per launch of the trivial kernel (ms_trivial[i]) and of the
+// library's fused AdamW kernel (ms_fused[i]) over one FP32 parameter and
+// gradient and two BF16 moments of n elements (20 bytes per element), at
+// resident-workgroup cap caps[i]: -1 for the library's rule
+// (sr::resident_cap), 0 for none, 1-12 for that many workgroups per CU;
+// resident[i] receives the workgroups per CU the fused launch allowed (the
+// runtime's occupancy calculator).  Each is averaged over `reps` launches
+// after two untimed ones; the two kernels alternate cap by cap.  n must be a
+// positive multiple of 512 with n / 512 <= 2^31 - 4096, 1 <= ncaps <= 32.
+// The buffers are allocated and freed here.  Returns 0, 1 for an
+// unsupported argument, or 2 for a HIP error.
+extern "C" int sr_launch_cap_sweep(uint64_t n, int reps, const int* caps, int ncaps, float* ms_trivial,
+                                   float* ms_fused, int* resident) {
+  if (!valid_streams(n, reps) || !caps || ncaps < 1 || ncaps > 32 || !ms_trivial || !ms_fused || !resident) return 1;
+  for (int i = 0; i < ncaps; ++i)
+    if (caps[i] < -1 || caps[i] > static_cast<int>(sr::kResidentCapMax)) return 1;
+  const uint32_t tiles = static_cast<uint32_t>(n / kTile);
+  const sr::LaunchShape shape = sr::launch_shape(tiles, kBlock);
+  auto fused = sr::adamw_kernel<sr::ENC_F32, sr::ENC_F32, sr::ENC_BF16_SR, sr::ENC_BF16_SR>;
+  auto trivial = streams<4, 4, 2, 2>;
+  char* slab = nullptr;
+  hipEvent_t start = nullptr, stop = nullptr;
+  int rc = 2;
+  do {
+    if (hipDeviceSynchronize() != hipSuccess || hipMalloc(reinterpret_cast<void**>(&slab), n * 12) != hipSuccess)
+      break;
+    float* p = reinterpret_cast<float*>(slab);
+    float* g = p + n;
+    char* m = slab + n * 8;
+    char* v = m + n * 2;
+    hipLaunchKernelGGL(fill_update_inputs, dim3(4096), dim3(256), 0, nullptr, p, g, n);
+    if (hipGetLastError() != hipSuccess || hipMemset(m, 0, n * 4) != hipSuccess) break;
+    if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess) break;
+    sr::AdamWArgs a{};
+    a.inline_row.ptr[0] = reinterpret_cast<uint64_t>(p);
+    a.inline_row.ptr[1] = reinterpret_cast<uint64_t>(g);
+    a.inline_row.ptr[2] = reinterpret_cast<uint64_t>(m);
+    a.inline_row.ptr[3] = reinterpret_cast<uint64_t>(v);
+    a.inline_row.numel = static_cast<int64_t>(n);
+    a.inline_row.tile_end = tiles;
+    a.inline_row.param_index = 7;
+    a.inline_row.flags = SR_ROW_VECTOR | SR_ROW_KEYED;
+    // lr 3e-4, betas (0.9, 0.999), eps 1e-8, weight decay 0.01 at step 1.
+    a.s = {0.9f, 0.999f, 0.1f, 0.001f, -3e-3f, 0.0316227766f, 1.0f - 3e-6f, 1e-8f, 1.0f / 0.0316227766f};
+    a.total_tiles = tiles;
+    bool failed = false;
+    for (int i = 0; i < ncaps && !failed; ++i) {
+      const uint32_t cap = caps[i] < 0 ? sr::resident_cap(tiles, kBlock, kLanes, 20, true) : caps[i];
+      for (int kind = 0; kind < 2 && !failed; ++kind) {
+        const void* fn = kind ? reinterpret_cast<const void*>(fused) : reinterpret_cast<const void*>(trivial);
+        const size_t lds = sr::cap_lds(fn, kBlock, cap);
+        if (kind && hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident[i], fn, kBlock, lds) != hipSuccess) {
+          failed = true;
+          break;
+        }
+        auto launch = [&] {
+          if (kind) hipLaunchKernelGGL(fused, dim3(shape.x, shape.y), dim3(kBlock), lds, nullptr, a);
+          else hipLaunchKernelGGL(trivial, dim3(shape.x, shape.y), dim3(kBlock), lds, nullptr, p, g, m, v, tiles);
+        };
+        launch();
+        launch();
+        float ms = 0.0f;
+        if (hipGetLastError() != hipSuccess || hipEventRecord(start, nullptr) != hipSuccess) {
+          failed = true;
+          break;
+        }
+        for (int r = 0; r < reps; ++r) launch();
+        if (hipGetLastError() != hipSuccess || hipEventRecord(stop, nullptr) != hipSuccess ||
+            hipEventSynchronize(stop) != hipSuccess || hipEventElapsedTime(&ms, start, stop) != hipSuccess) {
+          failed = true;
+          break;
+        }
+        (kind ? ms_fused : ms_trivial)[i] = ms / reps;
+      }
+    }
+    if (!failed) rc = 0;
+  } while (false);
+  if (start) (void)hipEventDestroy(start);
+  if (stop) (void)hipEventDestroy(stop);
+  (void)hipDeviceSynchronize();
+  if (slab) (void)hipFree(slab);
   return rc;
 }

@@ -5,7 +5,8 @@
 // workgroups walk whole chunks of 2^chunk_shift consecutive tiles.  It also
 // checks launch_shape: one row when the padded grid fits the per-dimension
 // work-item limit, otherwise rows of whole chunk rounds whose workgroups,
-// numbered row by row, still cover each tile exactly once.
+// numbered row by row, still cover each tile exactly once.  Finally it pins
+// resident_cap, the resident-workgroup cap of large optimizer launches.
 #include <cstdint>
 #include <cstdio>
 #include <vector>
@@ -107,6 +108,32 @@ int main() {
       ++failures;
     } else if (int rc = check_shape(big.tiles, big.block, 0xFFFFFFFFull, big.walk)) {
       std::printf("tiles %u block %u: failure %d\n", big.tiles, big.block, rc);
+      ++failures;
+    }
+  }
+  // resident_cap: round(80 KiB / tile bytes) for FP32-parameter launches of
+  // at least 2^16 tiles, when that is 1..12; otherwise none (0).
+  struct Cap { uint32_t tiles, block, bytes; bool fp32; uint32_t want; };
+  for (const Cap& c : {Cap{3022848u, 128u, 20u, true, 8u},   // north star: 80 KiB / 10 KiB
+                       Cap{65536u, 128u, 20u, true, 8u},     // smallest capped launch
+                       Cap{65535u, 128u, 20u, true, 0u},     // one tile fewer
+                       Cap{3022848u, 128u, 20u, false, 0u},  // BF16 parameters
+                       Cap{3022848u, 128u, 18u, true, 9u},   // 8.89
+                       Cap{3022848u, 128u, 16u, true, 10u},
+                       Cap{3022848u, 128u, 28u, true, 6u},   // 5.71
+                       Cap{3022848u, 128u, 24u, true, 7u},   // 6.67
+                       Cap{3022848u, 128u, 14u, true, 11u},  // 11.43
+                       Cap{3022848u, 128u, 13u, true, 12u},  // 12.31
+                       Cap{3022848u, 128u, 12u, true, 0u},   // 13.33: above the largest cap
+                       Cap{3022848u, 256u, 20u, true, 4u},
+                       Cap{3022848u, 1024u, 20u, true, 1u},
+                       Cap{3022848u, 1024u, 40u, true, 1u},  // 0.5 rounds up
+                       Cap{3022848u, 64u, 20u, true, 0u},    // 16
+                       Cap{0xFFFFFFFFu, 128u, 20u, true, 8u}}) {
+    const uint32_t got = sr::resident_cap(c.tiles, c.block, 4, c.bytes, c.fp32);
+    if (got != c.want) {
+      std::printf("resident_cap(%u, %u, 4, %u, %d) = %u, expected %u\n", c.tiles, c.block, c.bytes, c.fp32, got,
+                  c.want);
       ++failures;
     }
   }

@@ -79,33 +79,40 @@ def test_state_format_override_is_validated_before_anything_runs(value):
 
 
 def test_ceiling_helpers_refuse_bad_arguments_before_any_device_work():
-    """The placement sweep and the pattern ceiling check their arguments first (no GPU here)."""
+    """The pattern ceilings check their arguments first (no GPU here)."""
     import ctypes
 
     lib = ctypes.CDLL(str(bench.CEILING_LIBRARY))
-    lib.sr_stream_placements.restype = ctypes.c_int
-    lib.sr_stream_placements.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                         ctypes.c_int, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int,
-                                         ctypes.POINTER(ctypes.c_float)]
     lib.sr_stream_ceiling_p.restype = ctypes.c_int
     lib.sr_stream_ceiling_p.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
-    ms = (ctypes.c_float * 4)()
-
-    def placements(n, widths, gaps, reps=1):
-        array = (ctypes.c_uint64 * max(len(gaps), 1))(*gaps)
-        return lib.sr_stream_placements(n, *widths, reps, array, len(gaps), ms)
-
+    lib.sr_cast_ceiling.restype = ctypes.c_int
+    lib.sr_cast_ceiling.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.POINTER(ctypes.c_float)]
+    ms = ctypes.c_float()
     n = 512 * 1000
-    assert placements(n, (4, 4, 2, 2), [100]) == 1  # not a multiple of 256
-    assert placements(n, (4, 4, 2, 2), [(16 << 20) + 256]) == 1  # above 16 MiB
-    assert placements(n, (4, 4, 2, 2), []) == 1
-    assert placements(n + 1, (4, 4, 2, 2), [0]) == 1  # not whole tiles
-    assert placements(n, (4, 4, 3, 2), [0]) == 1  # no such pattern
-    assert placements(n, (4, 4, 2, 2), [0], reps=0) == 1
-    assert lib.sr_stream_ceiling_p(n, 2, 4, 2, 2, 1, ms) == 1
-    assert lib.sr_stream_ceiling_p(0, 4, 4, 2, 2, 1, ms) == 1
-    assert bench.PLACEMENT_GAPS[0] == 0 and all(g % 256 == 0 and g <= 16 << 20 for g in bench.PLACEMENT_GAPS)
+    assert lib.sr_stream_ceiling_p(n, 2, 4, 2, 2, 1, ctypes.byref(ms)) == 1  # no such pattern
+    assert lib.sr_stream_ceiling_p(n, 4, 4, 3, 2, 1, ctypes.byref(ms)) == 1
+    assert lib.sr_stream_ceiling_p(0, 4, 4, 2, 2, 1, ctypes.byref(ms)) == 1
+    assert lib.sr_stream_ceiling_p(n + 1, 4, 4, 2, 2, 1, ctypes.byref(ms)) == 1  # not whole tiles
+    assert lib.sr_stream_ceiling_p(n, 4, 4, 2, 2, 0, ctypes.byref(ms)) == 1  # no repetitions
+    assert lib.sr_cast_ceiling(2048 * 10, 3, 8, 1, ctypes.byref(ms)) == 1  # 3-byte output
+    assert lib.sr_cast_ceiling(2048 * 10, 2, 17, 1, ctypes.byref(ms)) == 1  # too many buffers
+    assert lib.sr_cast_ceiling(2048 * 10 + 1, 2, 8, 1, ctypes.byref(ms)) == 1
+    lib.sr_launch_cap_sweep.restype = ctypes.c_int
+    lib.sr_launch_cap_sweep.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.POINTER(ctypes.c_int), ctypes.c_int,
+                                        ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float),
+                                        ctypes.POINTER(ctypes.c_int)]
+    out = [(ctypes.c_float * 2)(), (ctypes.c_float * 2)(), (ctypes.c_int * 2)()]
+
+    def sweep(n, caps, reps=1):
+        return lib.sr_launch_cap_sweep(n, reps, (ctypes.c_int * max(len(caps), 1))(*caps), len(caps), *out)
+
+    assert sweep(n, [-2]) == 1  # below -1 (the rule)
+    assert sweep(n, [13]) == 1  # above the largest cap
+    assert sweep(n, []) == 1
+    assert sweep(n + 1, [0]) == 1  # not whole tiles
+    assert sweep(n, [0], reps=0) == 1
 
 
 @pytest.mark.parametrize("value,ok", [("1", True), ("1024", True), ("0", False), ("-1", False)])

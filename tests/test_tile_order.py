@@ -3,7 +3,8 @@
 tests/native/tile_order.cpp compiles csrc/sr_tile_order.h for the host and
 walks every workgroup of launches of 1..5000 tiles and of the configs' tile
 counts: each tile is covered exactly once, padding workgroups map past the
-last tile, and each XCD walks whole chunks of consecutive tiles.
+last tile, and each XCD walks whole chunks of consecutive tiles.  It also
+checks the resident-workgroup cap of large optimizer launches (resident_cap).
 """
 
 from __future__ import annotations
