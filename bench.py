@@ -25,7 +25,7 @@ per step), ``host_ms_submit`` (median host time until step() returns) and
 ``host_ms_wall`` (median host time until the step's work has finished).
 ``traffic`` comes from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
 measurement of the same workload, scaled by a copy-kernel calibration, when
-present.
+present; ``traffic_source`` names that summary and the build it measured.
 ``pattern_ceiling`` is the rate of a trivial-math kernel that moves exactly
 the same streams (widths, tile shape and order, non-temporal accesses) over
 the same number of elements (tests/native/stream_ceiling.hip), timed in the
@@ -863,12 +863,25 @@ def footprint_sweep(reps: int, rounds: int):
 
 
 def load_traffic(workload: str):
-    """HBM bytes per launch from the committed rocprofv3 FETCH/WRITE summary, or None."""
+    """HBM bytes per launch from the committed rocprofv3 FETCH/WRITE summary, and where they come from.
+
+    Returns (bytes, source) or (None, None): ``source`` names the summary
+    under profiles/ and the build commit it records.  The counters are not
+    collected in this run (rocprofv3 --pmc runs the program under the
+    profiler, one counter per pass).
+    """
     for path in sorted((ROOT / "profiles").glob(f"*_{workload}_hbm_traffic.md")):
+        value, build = None, None
         for line in path.read_text().splitlines():
             if line.startswith("hbm_bytes_per_launch:"):
-                return float(line.split(":", 1)[1])
-    return None
+                value = float(line.split(":", 1)[1])
+            elif line.startswith("build_commit:"):
+                build = line.split(":", 1)[1].strip()
+        if value is not None:
+            return value, {"profile": str(path.relative_to(ROOT)), "build_commit": build,
+                           "measured": "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, one pass each, "
+                                       "scaled by a 4 GiB copy's readings"}
+    return None, None
 
 
 def positive_int(text: str) -> int:
@@ -1029,7 +1042,7 @@ def main():
     bytes_per_launch = bpe * elements
     achieved = bytes_per_launch / (kernel_ms / 1e3) / 1e9
     # The committed counters were measured with the workload's own formats.
-    traffic = None if args.state_format else load_traffic(args.workload)
+    traffic, traffic_source = (None, None) if args.state_format else load_traffic(args.workload)
     dtype = "f32"
     result = {
         "metric": {
@@ -1069,6 +1082,7 @@ def main():
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "kernel_ms": kernel_ms,
             "step_ms_median": step_ms[len(step_ms) // 2],
             "step_ms_min": step_ms[0],
