@@ -238,3 +238,13 @@ def test_validation_of_casts(dtype, rule):
     finals = [[sr_oracle.cast(x, dtype=dtype, rounding=rule, seed=7, offset=6)]]
     if rule == "stochastic":  # another counter base draws other bits
         assert bench.validate(spec, samples, finals, steps=1)["mismatches"] > 0
+
+
+def test_traffic_comes_with_its_source():
+    """The bench line's HBM traffic is read from a committed summary, which it names with its build."""
+    traffic, source = bench.load_traffic("north_star")
+    assert traffic is not None and traffic > 30e9
+    assert source["profile"] == "profiles/adamw_kernel_north_star_hbm_traffic.md"
+    assert source["build_commit"] and len(source["build_commit"]) >= 7
+    assert (ROOT / source["profile"]).exists()
+    assert bench.load_traffic("no_such_workload") == (None, None)
