@@ -221,9 +221,15 @@ int sr_adamw_multi(const sr_row* rows, const uint32_t* tile_rows, const float* r
  * work.  The array is one per GPU and keeps the last call's contents: calls
  * that overlap on one GPU (on different streams or threads) race, so a
  * caller serializes them, for example on one stream.  The stream must belong
- * to the current device.  Pageable `rows`/`row_scalars` may be reused when
- * the call returns; pinned ones must stay unchanged until the stream has
- * passed the call. */
+ * to the current device.  Eager calls: pageable `rows`/`row_scalars` may be
+ * reused when the call returns; pinned ones must stay unchanged until the
+ * stream has passed the call.  Under HIP stream capture the two table copies
+ * become graph nodes that read the host tables again at every replay: the
+ * tables must then be pinned host memory (hipHostMalloc) that stays valid
+ * and unchanged for as long as the graph can replay, and pageable ones fail
+ * with SR_ERR_ARGUMENT before anything is recorded.  Each replay restages
+ * the tables in the scratch, so replays race with other calls on the GPU
+ * as calls do. */
 int sr_adamw_multi_noalloc(const sr_row* rows, const float* row_scalars, int nrows, uint32_t total_tiles,
                            int p_dtype, int g_dtype, int m_dtype, int m_rule, int v_dtype, int v_rule,
                            const sr_adamw_hparams* hp, uint64_t seed, uint64_t rng_step, int block_size,

@@ -200,6 +200,29 @@ __global__ __launch_bounds__(kFillBlock) void fill_tile_rows(const sr_row* rows,
   tile_rows[t] = static_cast<uint32_t>(lo);
 }
 
+// Under stream capture the copies of the host tables become graph nodes that
+// read the tables again at every replay, so they must be pinned (page-locked)
+// host memory that outlives the graph; pageable tables are refused before
+// anything is recorded.  Eager calls take either kind.
+int check_capture_tables(hipStream_t stream, const void* rows, const void* row_scalars) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  hipError_t err = hipStreamIsCapturing(stream, &status);
+  if (err != hipSuccess) return hip_fail(err, "hipStreamIsCapturing");
+  if (status == hipStreamCaptureStatusNone) return SR_OK;
+  const void* tables[2] = {rows, row_scalars};
+  for (const void* table : tables) {
+    if (!table) continue;
+    hipPointerAttribute_t attributes{};
+    err = hipPointerGetAttributes(&attributes, table);
+    if (err != hipSuccess) (void)hipGetLastError();  // an unknown pointer: not pinned
+    if (err != hipSuccess || attributes.type != hipMemoryTypeHost)
+      return fail(SR_ERR_ARGUMENT,
+                  "under stream capture, rows and row_scalars must be pinned host memory that stays unchanged "
+                  "while the graph can replay");
+  }
+  return SR_OK;
+}
+
 // The checks sr_adamw_multi leaves to its caller, made on the host copy.
 int check_host_rows(const sr_row* rows, const float* row_scalars, int nrows, uint32_t total_tiles,
                     int64_t tile_elements) {
@@ -433,6 +456,7 @@ int sr_adamw_multi_noalloc(const sr_row* rows, const float* row_scalars, int nro
   const int64_t tile_elements =
       static_cast<int64_t>(block_size) * sr::lane_elements(param_enc(pi), param_enc(gi), me, ve);
   if (int rc = check_host_rows(rows, row_scalars, nrows, total_tiles, tile_elements)) return rc;
+  if (int rc = check_capture_tables(static_cast<hipStream_t>(stream), rows, row_scalars)) return rc;
   unsigned char* base = nullptr;
   if (int rc = scratch_base(stream, &base)) return rc;
   sr_row* rows_dev = reinterpret_cast<sr_row*>(base);

@@ -8,6 +8,12 @@ identical byte for byte on two calls in a row, the second with fewer rows and
 tiles (and per-row step scalars), so stale scratch contents from the first
 call would show.  Oversized and malformed tables are refused on the host
 before any device work, leaving every tensor unchanged.
+
+Under HIP graph capture the entry takes pinned host tables: a captured call
+is replayed three times, each time from the same initial tensors and after
+an eager call on other tables has overwritten the scratch, and every replay
+must equal the eager sr_adamw_multi step.  Pageable tables are refused under
+capture before anything is recorded.
 """
 
 from __future__ import annotations
@@ -173,3 +179,74 @@ def test_noalloc_refuses_oversized_and_malformed_tables(cuda):
     for row, saved in zip(rows, before):
         for t, s in zip(row, saved):
             assert torch.equal(t.view(torch.uint8), s.view(torch.uint8))
+
+
+def _pinned(array):
+    """A page-locked host copy of a numpy array's bytes, as a torch tensor."""
+    return torch.from_numpy(np.ascontiguousarray(array).view(np.uint8).reshape(-1)).pin_memory()
+
+
+def test_noalloc_under_graph_capture_replays_like_eager_calls(cuda):
+    formats = FORMATS[1]
+    dtypes = (torch.float32, torch.float32, formats[0][0], formats[1][0])
+    sizes, first_index, steps, step = [70_001, 4099, -2053, 1, 512], 3, [1, 4, 2, 9, 3], 4
+    ours = _bucket(cuda, sizes, dtypes, seed=77)
+    initial = _clone(ours)
+    theirs = _clone(ours)
+    records, tile_rows = _tables(ours, first_index)
+    records_theirs, _ = _tables(theirs, first_index)
+    scalars = _row_scalars(steps)
+    _launch_device_tables(cuda, theirs, formats, records_theirs, tile_rows, scalars, step)
+    rows_pinned, scalars_pinned = _pinned(records), _pinned(scalars)
+    other = _bucket(cuda, [9000, 257], dtypes, seed=78)
+    other_records, other_tiles = _tables(other, 0)
+    lib = _lib.library()
+    hp = adamw_hparams(HYPER["lr"], HYPER["beta1"], HYPER["beta2"], HYPER["eps"], HYPER["weight_decay"], step)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        status = lib.sr_adamw_multi_noalloc(
+            rows_pinned.data_ptr(), scalars_pinned.data_ptr(), len(records), len(tile_rows), *_codes(ours, formats),
+            ctypes.byref(hp), SEED, RNG_STEP, BLOCK, _lib.stream_handle(cuda))
+    _lib.check("sr_adamw_multi_noalloc (captured)", status)
+    for replay in range(3):
+        # Eager work between replays: the tensors back to their initial bytes,
+        # and a call on other tables that leaves them in the scratch.
+        for row, start in zip(ours, initial):
+            for t, t0 in zip(row, start):
+                t.copy_(t0)
+        _lib.check("sr_adamw_multi_noalloc", _launch_noalloc(cuda, other, formats, other_records, len(other_tiles),
+                                                             None, 1))
+        graph.replay()
+        torch.cuda.synchronize()
+        for r, (a, b) in enumerate(zip(ours, theirs)):
+            for name, x, y in zip(("parameter", "gradient", "exp_avg", "exp_avg_sq"), a, b):
+                assert_bits_or_nan(x.cpu(), y.cpu(), f"replay {replay + 1}, row {r}: {name}")
+    del graph
+    torch.cuda.synchronize()
+
+
+def test_noalloc_refuses_pageable_tables_under_capture(cuda):
+    formats = FORMATS[0]
+    rows = _bucket(cuda, [4099, 600], (torch.float32, torch.float32, torch.bfloat16, torch.bfloat16), seed=6)
+    before = [[t.clone() for t in row] for row in rows]
+    records, tile_rows = _tables(rows, 0)
+    lib = _lib.library()
+    hp = adamw_hparams(HYPER["lr"], HYPER["beta1"], HYPER["beta2"], HYPER["eps"], HYPER["weight_decay"], 1)
+    marker = torch.zeros(1, device=cuda)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        status = lib.sr_adamw_multi_noalloc(
+            records.ctypes.data, None, len(records), len(tile_rows), *_codes(rows, formats), ctypes.byref(hp),
+            SEED, RNG_STEP, BLOCK, _lib.stream_handle(cuda))
+        marker.add_(1)  # the graph records this kernel and nothing of the refused call
+    assert status == 1, status  # SR_ERR_ARGUMENT
+    assert "pinned host memory" in lib.sr_last_error().decode(), lib.sr_last_error()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert marker.item() == 1
+    for row, saved in zip(rows, before):
+        for t, s in zip(row, saved):
+            assert torch.equal(t.view(torch.uint8), s.view(torch.uint8))
+    del graph
