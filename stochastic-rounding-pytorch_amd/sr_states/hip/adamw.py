@@ -103,11 +103,12 @@ def adamw_step_any_hyperparameters_(
     launch's: the division by sqrt(1 - beta2^step) is exact for constants
     in [2^-27, 1], which every beta2 in [0, 1) gives, and the library
     refuses others with an error.  beta1 = 1 divides by zero here as in the
-    reference.  Its callers run under no_grad; the launch itself records
-    nothing for autograd.
+    reference.  ``step`` may be any real number of at least 1, which the
+    reference's bias corrections take (its callers check it).  Its callers
+    run under no_grad; the launch itself records nothing for autograd.
     """
     codes = resolve_native_codes(_STATE_NAMES, (exp_avg, exp_avg_sq), formats, None, DEFAULT_BLOCK_SIZE)
-    scalars = adamw_scalars(lr, beta1, beta2, eps, weight_decay, _positive_step(step))
+    scalars = adamw_scalars(lr, beta1, beta2, eps, weight_decay, step)
     correction = scalars[5]  # sqrt(1 - beta2**step): complex when beta2**step > 1
     if isinstance(correction, complex) or not 0 < correction <= 1:
         raise ValueError(

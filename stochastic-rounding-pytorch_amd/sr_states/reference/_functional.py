@@ -18,8 +18,11 @@ reference's contract from there without any CPU arithmetic:
   give the same bytes.
 
 Parameters outside FP32/BF16 are updated in an FP32 copy and converted back
-with ``Tensor.to`` (round to nearest even), which is the reference's own
-final step; gradients outside FP32/BF16 are widened with ``Tensor.float``.
+with ``Tensor.to`` (round to nearest even for floating-point dtypes,
+truncation for integer ones), which is the reference's own final step;
+gradients outside FP32/BF16 are widened with ``Tensor.float``.  So integer
+and boolean inputs are read as the reference's ``.float()`` reads them;
+complex ones are refused (``.float()`` would drop their imaginary parts).
 """
 
 from __future__ import annotations
@@ -45,10 +48,10 @@ def check_inputs(tensors) -> None:
                 "functional state updates take local tensors: pass each DTensor's to_local() and "
                 "the flat index of the shard's first element as offset"
             )
+        if tensor.dtype.is_complex:
+            raise TypeError(f"expected real tensors, got {tensor.dtype}")
         if tensor.device.type != "cuda":
             raise ValueError(f"sr_states updates run on the GPU; got a {tensor.device.type} tensor")
-        if not tensor.dtype.is_floating_point:
-            raise TypeError(f"expected floating-point tensors, got {tensor.dtype}")
 
 
 def kernel_ready(parameter, gradient, states, formats) -> bool:

@@ -13,9 +13,15 @@ Like the reference, they check no hyperparameter: any learning rate,
 epsilon and weight decay are taken (a negative learning rate ascends).  The
 one limit is the launch's exact division by sqrt(1 - beta2**step), which
 takes every beta2 in [0, 1); beta1 = 1 divides by zero as in the reference.
+``step`` is any real number of at least 1 (a Python or NumPy integer or
+float), which only the bias corrections use, as in the reference
+(reference/adamw.py:73-84); a tensor is refused, where the reference's
+``addcdiv_`` fails on one.
 """
 
 from __future__ import annotations
+
+import numbers
 
 import torch
 
@@ -27,8 +33,8 @@ _NAMES = ("exp_avg", "exp_avg_sq")
 
 
 def _formats(step, state_dtype, formats, rounding):
-    if not isinstance(step, int) or isinstance(step, bool):
-        raise TypeError("step must be an integer")
+    if not isinstance(step, numbers.Real):
+        raise TypeError(f"step must be a real number, not {type(step).__name__}")
     if step < 1:
         raise ValueError("step must be at least 1")
     return resolve_formats(_NAMES, formats, state_dtype=state_dtype, rounding=rounding)

@@ -9,6 +9,7 @@ tensor they raise before any work instead of computing.
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -128,8 +129,18 @@ def test_argument_errors_come_before_device_checks():
     tensors = _adamw_inputs()
     with pytest.raises(ValueError, match="step must be at least 1"):
         functional.adamw_step(*tensors, **{**ADAMW, "step": 0})
-    with pytest.raises(TypeError, match="step must be an integer"):
-        functional.adamw_step(*tensors, **{**ADAMW, "step": 1.0})
+    with pytest.raises(TypeError, match="step must be a real number"):
+        functional.adamw_step(*tensors, **{**ADAMW, "step": torch.tensor(3)})
+    with pytest.raises(TypeError, match="step must be a real number"):
+        functional.adamw_step(*tensors, **{**ADAMW, "step": "3"})
+    with pytest.raises(ValueError, match="step must be at least 1"):
+        functional.adamw_step(*tensors, **{**ADAMW, "step": np.int64(0)})
+    # Steps the reference takes reach the device check (no CPU path here).
+    for step in (np.int64(3), 2.5, np.float32(7.0), True):
+        with pytest.raises(ValueError, match="on the GPU"):
+            functional.adamw_step(*tensors, **{**ADAMW, "step": step})
+    with pytest.raises(TypeError, match="expected real tensors"):
+        functional.adamw_step(tensors[0].to(torch.complex64), *tensors[1:], **ADAMW)
     with pytest.raises(ValueError, match="cannot be combined"):
         functional.adamw_step(*tensors, formats=StateFormat(torch.bfloat16), state_dtype=torch.float16, **ADAMW)
     with pytest.raises(ValueError, match="no rounding"):

@@ -17,6 +17,7 @@ and tests/test_triton_states.py:85-113 of the reference.
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 from conftest import assert_bits_or_nan, raw_bits
@@ -346,6 +347,46 @@ def test_reference_adamw_takes_any_hyperparameters_as_the_reference_does(cuda, h
     _assert_all(out, [want[0], want[2], want[3]], f"adamw_step {hyper}")
     with pytest.raises(ValueError, match="invalid"):
         sr_states.hip_adamw_step_(*got, formats=_fmts(formats), seed=KEY, offset=OFFSET, **options)
+
+
+@pytest.mark.parametrize("step", [np.int64(7), 7.0, 2.5, np.float32(3.0), True], ids=repr)
+def test_reference_adamw_takes_any_real_step_as_the_reference_does(cuda, step):
+    """reference/adamw.py:73-84 checks only step >= 1 and uses it in the bias corrections."""
+    formats = FORMAT_SETS[0]
+    options = {**ADAMW, "step": step}
+    p, g, (m, v) = _inputs(2003, torch.float32, torch.float32, [f[0] for f in formats], seed=19)
+    want = [t.clone() for t in (p, g, m, v)]
+    c_oracle.adamw_step_(*want, formats=formats, seed=KEY, offset=OFFSET, **options)
+    out = functional.adamw_step(*(t.to(cuda) for t in (p, g, m, v)), formats=_fmts(formats), seed=KEY,
+                                offset=OFFSET, **options)
+    _assert_all(out, [want[0], want[2], want[3]], f"step {step!r}")
+
+
+def test_reference_adamw_reads_integer_and_boolean_tensors_through_float(cuda):
+    """reference/adamw.py:79-89 reads every input with ``.float()``, returns the parameter
+    through ``.to(parameter.dtype)`` (truncation for integers) and each moment through its
+    format; the in-place update copies them back into the tensors' own dtypes."""
+    formats = FORMAT_SETS[0]
+    gen = torch.Generator().manual_seed(13)
+    n = 1999
+    p = torch.randint(-60, 60, (n,), generator=gen, dtype=torch.int32)
+    g = torch.randint(0, 2, (n,), generator=gen).bool()
+    m = torch.randint(-2, 3, (n,), generator=gen, dtype=torch.int16)
+    v = torch.randint(0, 4, (n,), generator=gen, dtype=torch.int64)
+    new_p, new_m, new_v = functional.adamw_step(*(t.to(cuda) for t in (p, g, m, v)), formats=_fmts(formats),
+                                                seed=KEY, offset=OFFSET, **ADAMW)
+    p32, g32, m32, v32 = (t.float() for t in (p, g, m, v))
+    c_oracle.adamw_step_(p32, g32, m32, v32, formats=((torch.float32, "nearest"),) * 2, seed=KEY, offset=OFFSET,
+                         **ADAMW)
+    assert new_p.dtype == torch.int32 and torch.equal(new_p.cpu(), p32.to(torch.int32))
+    for k, (got, wide, (dtype, rule)) in enumerate(zip((new_m, new_v), (m32, v32), formats)):
+        want = c_oracle.cast(wide, dtype=dtype, rounding=rule, seed=sr_oracle.state_key(KEY, k), offset=OFFSET)
+        assert_bits_or_nan(got.cpu(), want, f"state {k}")
+    tensors = [t.to(cuda) for t in (p, g, m, v)]
+    functional.adamw_step_(*tensors, formats=_fmts(formats), seed=KEY, offset=OFFSET, **ADAMW)
+    assert torch.equal(tensors[0].cpu(), new_p.cpu())
+    assert torch.equal(tensors[2].cpu(), new_m.cpu().to(torch.int16))
+    assert torch.equal(tensors[3].cpu(), new_v.cpu().to(torch.int64))
 
 
 def test_reference_adamw_refuses_only_what_the_launch_cannot_divide_by(cuda):
