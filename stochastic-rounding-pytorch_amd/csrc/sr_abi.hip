@@ -97,13 +97,18 @@ int launch(const void* fn, int block, uint32_t tiles, void* arg, void* stream, u
   return SR_OK;
 }
 
+// Whether an encoding rounds stochastically to FP16 or FP8.
+bool minifloat_sr(int enc) { return enc == sr::ENC_F16_SR || enc == sr::ENC_E4M3_SR || enc == sr::ENC_E5M2_SR; }
+
 // Resident-workgroup cap of an AdamW launch (sr::resident_cap).
 uint32_t adamw_cap(int pi, int gi, int me, int ve, int block, uint32_t tiles) {
   const int bytes = 2 * sr::enc_bytes(param_enc(pi)) + sr::enc_bytes(param_enc(gi)) + 2 * sr::enc_bytes(me) +
                     2 * sr::enc_bytes(ve);
+  const uint32_t in_flight = minifloat_sr(me) && minifloat_sr(ve) ? sr::kInFlightBytesPerCuTwoMinifloatSr
+                                                                  : sr::kInFlightBytesPerCu;
   return sr::resident_cap(tiles, static_cast<uint32_t>(block),
                           static_cast<uint32_t>(sr::lane_elements(param_enc(pi), param_enc(gi), me, ve)),
-                          static_cast<uint32_t>(bytes), pi == 0);
+                          static_cast<uint32_t>(bytes), pi == 0, in_flight);
 }
 
 // Resident-workgroup cap of a momentum-SGD launch.

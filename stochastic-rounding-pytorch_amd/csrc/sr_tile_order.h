@@ -79,31 +79,40 @@ SR_HOST_DEVICE inline LaunchShape launch_shape(uint32_t tiles, uint32_t block,
 // use few registers, so 16 of their 128-lane workgroups fit on a CU, and
 // that many keep more memory requests in flight than HBM can serve: the
 // surplus only adds contention.  Measured on MI355X (every cap exact,
-// interleaved in one process), the rate peaks with about 80 KiB of tiles
-// in flight per CU, i.e. cap = round(80 KiB / tile bytes):
-//   north star (FP32 p/g, BF16-SR m/v, 20 B):  6.04 -> 6.46 TB/s at 8
+// interleaved in one process, through the library's multi-tensor launches),
+// the rate peaks with about 80 KiB of tiles in flight per CU, i.e. cap =
+// round(80 KiB / tile bytes):
+//   north star (FP32 p/g, BF16-SR m/v, 20 B):  6.21 -> 6.40 TB/s at 8
 //   2^26-element tensor, same streams:           6.45 -> 6.71 at 8
-//   E4M3 m + BF16 v (18 B): 6.17 -> 6.41 at 9;  BF16 g (18 B): 6.33 -> 6.61 at 9
-//   SGDM, FP16 momentum (16 B): 6.37 -> 6.61 at 8 (6.49 at the rule's 10)
-//   FP32 moments (28 B): 5.91 -> 6.47 at 5 (6.31 at the rule's 6)
+//   E4M3-SR m + BF16-SR v (18 B): 6.20 -> 6.38 at 9
+//   SGDM, FP16-SR momentum (16 B): 6.31 -> 6.44 at the rule's 10 (6.53 at 9)
+//   FP32 moments (28 B): 6.03 -> 6.18-6.26 at the rule's 6 (6.24 at 7)
+// AdamW launches whose two moments both round stochastically to FP16 or FP8
+// spend longer in each workgroup's arithmetic (two minifloat encoders per
+// element) and peak nearer 96 KiB: FP16-SR m/v (20 B) 6.18 -> 6.33 at 10
+// (6.20 at 8), E4M3-SR m/v (16 B) 6.22 -> 6.35 at 12 (6.25 at 10), E5M2-SR
+// m/v 6.28 -> 6.34 at 12 (6.22 at 10).
 // Launches with BF16 parameters spend more of a workgroup's life in
 // arithmetic; caps of 11 to 15 moved them by under 1%, so they stay
 // uncapped, as do launches of fewer than 2^16 tiles (2^25 elements at 128
 // lanes), whose tail the cap lengthens (2^24 elements: 6.50 -> 6.46;
 // 2^25: 6.53 -> 6.62), and the casts (every cap slower).
 constexpr uint32_t kInFlightBytesPerCu = 80u * 1024u;
+constexpr uint32_t kInFlightBytesPerCuTwoMinifloatSr = 96u * 1024u;
 constexpr uint32_t kResidentCapMinTiles = 1u << 16;
 constexpr uint32_t kResidentCapMax = 12;
 
 // Workgroups per CU to leave resident for an optimizer launch of `tiles`
 // tiles of `block` lanes times `lanes` elements, moving `bytes_per_element`
-// bytes per element, or 0 for no cap.
+// bytes per element with `in_flight` bytes of tiles in flight per CU, or 0
+// for no cap.
 SR_HOST_DEVICE inline uint32_t resident_cap(uint32_t tiles, uint32_t block, uint32_t lanes,
-                                            uint32_t bytes_per_element, bool fp32_params) {
+                                            uint32_t bytes_per_element, bool fp32_params,
+                                            uint32_t in_flight = kInFlightBytesPerCu) {
   if (!fp32_params || tiles < kResidentCapMinTiles) return 0;
   const uint64_t tile_bytes = static_cast<uint64_t>(block) * lanes * bytes_per_element;
   if (tile_bytes == 0) return 0;
-  const uint64_t cap = (kInFlightBytesPerCu + tile_bytes / 2) / tile_bytes;
+  const uint64_t cap = (in_flight + tile_bytes / 2) / tile_bytes;
   return cap >= 1 && cap <= kResidentCapMax ? static_cast<uint32_t>(cap) : 0u;
 }
 

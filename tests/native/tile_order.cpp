@@ -111,8 +111,8 @@ int main() {
       ++failures;
     }
   }
-  // resident_cap: round(80 KiB / tile bytes) for FP32-parameter launches of
-  // at least 2^16 tiles, when that is 1..12; otherwise none (0).
+  // resident_cap: round(in-flight bytes / tile bytes) for FP32-parameter
+  // launches of at least 2^16 tiles, when that is 1..12; otherwise none (0).
   struct Cap { uint32_t tiles, block, bytes; bool fp32; uint32_t want; };
   for (const Cap& c : {Cap{3022848u, 128u, 20u, true, 8u},   // north star: 80 KiB / 10 KiB
                        Cap{65536u, 128u, 20u, true, 8u},     // smallest capped launch
@@ -134,6 +134,15 @@ int main() {
     if (got != c.want) {
       std::printf("resident_cap(%u, %u, 4, %u, %d) = %u, expected %u\n", c.tiles, c.block, c.bytes, c.fp32, got,
                   c.want);
+      ++failures;
+    }
+  }
+  // 96 KiB in flight (AdamW with two stochastic FP16/FP8 moments).
+  struct Cap96 { uint32_t bytes, want; };
+  for (const Cap96& c : {Cap96{20u, 10u}, Cap96{16u, 12u}, Cap96{18u, 11u}, Cap96{28u, 7u}, Cap96{15u, 0u}}) {
+    const uint32_t got = sr::resident_cap(3022848u, 128u, 4, c.bytes, true, sr::kInFlightBytesPerCuTwoMinifloatSr);
+    if (got != c.want) {
+      std::printf("resident_cap(96 KiB, %u B) = %u, expected %u\n", c.bytes, got, c.want);
       ++failures;
     }
   }
