@@ -9,8 +9,10 @@ tiles (and per-row step scalars), so stale scratch contents from the first
 call would show.  Oversized and malformed tables are refused on the host
 before any device work, leaving every tensor unchanged.
 
-Under HIP graph capture the entry takes pinned host tables: a captured call
-is replayed three times, each time from the same initial tensors and after
+The first call's bucket, and the captured one, pass 2^16 tiles, so their
+FP32-parameter launches run with the resident-workgroup cap.  Under HIP
+graph capture the entry takes pinned host tables: a captured call is
+replayed three times, each time from the same initial tensors and after
 an eager call on other tables has overwritten the scratch, and every replay
 must equal the eager sr_adamw_multi step.  Pageable tables are refused under
 capture before anything is recorded.
@@ -127,7 +129,9 @@ def test_noalloc_equals_device_table_launch_on_two_calls(cuda, formats, p_dtype,
     dtypes = (p_dtype, g_dtype, formats[0][0], formats[1][0])
     calls = [
         # (sizes, first parameter index, per-row steps or None, step)
-        ([2_000_003, 4099, -2053, 1, 512, 70_000, 129], 0, None, 5),
+        # 2^25 + 2^20 elements: past 2^16 tiles, so FP32-parameter launches
+        # run with their resident-workgroup cap.
+        ([(1 << 25) + (1 << 20), 2_000_003, 4099, -2053, 1, 512, 70_000, 129], 0, None, 5),
         ([1027, -515, 3], 9, [1, 7, 2], 2),
     ]
     for call, (sizes, first_index, steps, step) in enumerate(calls):
@@ -189,7 +193,9 @@ def _pinned(array):
 def test_noalloc_under_graph_capture_replays_like_eager_calls(cuda):
     formats = FORMATS[1]
     dtypes = (torch.float32, torch.float32, formats[0][0], formats[1][0])
-    sizes, first_index, steps, step = [70_001, 4099, -2053, 1, 512], 3, [1, 4, 2, 9, 3], 4
+    # The first row takes the bucket past 2^16 tiles: the captured launch
+    # carries the resident-workgroup cap.
+    sizes, first_index, steps, step = [(1 << 25) + 3, 70_001, 4099, -2053, 1, 512], 3, [1, 4, 2, 9, 3, 5], 4
     ours = _bucket(cuda, sizes, dtypes, seed=77)
     initial = _clone(ours)
     theirs = _clone(ours)
