@@ -8,7 +8,8 @@ and gradient, BF16 stochastic moments) on one tensor of 2^28 elements
 (5.4 GB) with the rule's cap and with none, interleaved over three rounds:
 the occupancy calculator must report the rule's 8 workgroups per CU, and
 the capped kernel must be at least as fast as the uncapped one (on MI355X
-it is 3-4% faster at this footprint).
+it is 3-4% faster at this footprint).  The single-tensor entries, capped
+past 2^16 tiles, are held to the C oracle.
 """
 
 from __future__ import annotations
@@ -18,6 +19,7 @@ import statistics
 from pathlib import Path
 
 import pytest
+import torch
 
 pytestmark = pytest.mark.gpu
 
@@ -44,3 +46,52 @@ def test_capped_fused_kernel_is_at_least_as_fast_as_uncapped(cuda):
     capped_ms, uncapped_ms = statistics.median(capped), statistics.median(uncapped)
     assert capped_ms <= uncapped_ms, (
         f"capped {rate(capped_ms):.0f} GB/s against uncapped {rate(uncapped_ms):.0f} GB/s")
+
+
+CHUNK = 4099
+
+
+@pytest.mark.parametrize("kind", ["adamw", "sgdm"])
+def test_capped_single_tensor_launches_equal_the_oracle(cuda, kind):
+    """The single-tensor entries past 2^16 tiles (capped) against the C oracle, sampled chunks.
+
+    2^25 + 5 elements make 65537 tiles of 512: the launch reserves its LDS.
+    Chunks at the head, inside and at the tail (a partial last tile) must
+    equal the oracle's replay of the same elements with the chunk start as
+    the counter offset, parameters and states byte for byte.
+    """
+    import sr_states
+    from conftest import assert_bits_or_nan
+
+    from oracle import c_oracle
+
+    n = (1 << 25) + 5
+    key, offset = 0xA5A5F00D, 12_345
+    gen = torch.Generator(device=cuda).manual_seed(23)
+    p = torch.empty(n, device=cuda).normal_(std=0.02, generator=gen)
+    g = torch.empty(n, device=cuda).normal_(std=1e-3, generator=gen)
+    starts = [0, (n // 3) * 2 + 7, n - CHUNK]
+    before = {s: (p[s:s + CHUNK].cpu(), g[s:s + CHUNK].cpu()) for s in starts}
+    if kind == "adamw":
+        formats = ((torch.float8_e4m3fn, "stochastic"), (torch.bfloat16, "stochastic"))
+        states = [torch.zeros(n, device=cuda, dtype=d) for d, _ in formats]
+        hyper = dict(lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, step=3)
+        sr_states.hip_adamw_step_(p, g, *states, seed=key, offset=offset,
+                                  formats=tuple(sr_states.StateFormat(d, r) for d, r in formats), **hyper)
+    else:
+        formats = ((torch.float16, "stochastic"),)
+        states = [torch.zeros(n, device=cuda, dtype=torch.float16)]
+        hyper = dict(lr=0.1, momentum_factor=0.9)
+        sr_states.hip_sgdm_step_(p, g, *states, seed=key, offset=offset,
+                                 formats=(sr_states.StateFormat(torch.float16, "stochastic"),), **hyper)
+    torch.cuda.synchronize()
+    for start, (p_ref, g_ref) in before.items():
+        refs = [torch.zeros(CHUNK, dtype=d) for d, _ in formats]
+        if kind == "adamw":
+            c_oracle.adamw_step_(p_ref, g_ref, *refs, formats=formats, seed=key, offset=offset + start, **hyper)
+        else:
+            c_oracle.sgdm_step_(p_ref, g_ref, *refs, formats=formats, seed=key, offset=offset + start, **hyper)
+        sl = slice(start, start + CHUNK)
+        assert_bits_or_nan(p[sl].cpu(), p_ref, f"{kind} parameter at {start}")
+        for k, (state, ref) in enumerate(zip(states, refs)):
+            assert_bits_or_nan(state[sl].cpu(), ref, f"{kind} state {k} at {start}")
