@@ -28,24 +28,26 @@ constexpr int kCapMaxBlock = 1024;
 // workgroups, the answer depends on the LDS alone and is shared.  A kernel
 // whose registers already hold it to `cap` needs none (and the shared size
 // changes nothing for it).  0 when the calculator fails: the launch then
-// runs uncapped.
+// runs uncapped, and the failure is cleared from the runtime's last error so
+// that no later, unrelated error check reports it.
 inline size_t cap_lds(const void* fn, int block, uint32_t cap) {
   static std::atomic<uint32_t> known[kCapMaxBlock / 64][kResidentCapMax + 1];
   if (cap == 0 || cap > kResidentCapMax || block < 64 || block > kCapMaxBlock || block % 64) return 0;
   std::atomic<uint32_t>& slot = known[block / 64 - 1][cap];
   const uint32_t kept = slot.load(std::memory_order_relaxed);
   if (kept != 0) return static_cast<size_t>(kept - 1) * 256;
+  auto resident_with = [&](size_t lds, int* resident) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(resident, fn, block, lds) == hipSuccess) return true;
+    (void)hipGetLastError();
+    return false;
+  };
   int uncapped = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&uncapped, fn, block, 0) != hipSuccess ||
-      uncapped <= static_cast<int>(cap))
-    return 0;
+  if (!resident_with(0, &uncapped) || uncapped <= static_cast<int>(cap)) return 0;
   uint32_t lo = 1, hi = kLdsPerCu / 256;
   while (lo < hi) {
     const uint32_t mid = (lo + hi) / 2;
     int resident = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, fn, block, static_cast<size_t>(mid) * 256) !=
-        hipSuccess)
-      return 0;
+    if (!resident_with(static_cast<size_t>(mid) * 256, &resident)) return 0;
     if (resident <= static_cast<int>(cap)) hi = mid;
     else lo = mid + 1;
   }
