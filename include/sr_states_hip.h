@@ -17,6 +17,12 @@
  *     the memory alive until the stream has consumed it.
  *   - Counters are 32-bit: every seed/offset/step word is taken modulo 2^32,
  *     exactly as the reference masks them (sr_states/_hash.py:5-50).
+ *   - Optimizer launches of 2^16 tiles or more with FP32 parameters reserve
+ *     dynamic LDS that their kernels never touch, to keep about 80 KiB of
+ *     tiles in flight per CU (96 KiB for AdamW with two FP16/FP8
+ *     stochastic moments); kernels of other streams running beside such a
+ *     launch find that LDS taken on the CUs it occupies.  Results do not
+ *     depend on it.
  */
 #ifndef SR_STATES_HIP_H
 #define SR_STATES_HIP_H
