@@ -8,8 +8,9 @@ and gradient, BF16 stochastic moments) on one tensor of 2^28 elements
 (5.4 GB) with the rule's cap and with none, interleaved over three rounds:
 the occupancy calculator must report the rule's 8 workgroups per CU, and
 the capped kernel must be at least as fast as the uncapped one (on MI355X
-it is 3-4% faster at this footprint).  The single-tensor entries, capped
-past 2^16 tiles, are held to the C oracle.
+it is 3-4% faster at this footprint).  The single-tensor entries and the
+optimizers at 256-, 512- and 1024-lane workgroups, capped past 2^16 tiles,
+are held to the C oracle.
 """
 
 from __future__ import annotations
@@ -95,3 +96,45 @@ def test_capped_single_tensor_launches_equal_the_oracle(cuda, kind):
         assert_bits_or_nan(p[sl].cpu(), p_ref, f"{kind} parameter at {start}")
         for k, (state, ref) in enumerate(zip(states, refs)):
             assert_bits_or_nan(state[sl].cpu(), ref, f"{kind} state {k} at {start}")
+
+
+@pytest.mark.parametrize("kind, block_size", [("adamw", 256), ("adamw", 1024), ("sgdm", 512)])
+def test_capped_launches_of_other_workgroup_sizes_equal_the_oracle(cuda, kind, block_size):
+    """The optimizers with a non-default workgroup size, past 2^16 tiles (so capped: 4 workgroups
+    of 256 lanes and 1 of 1024 for AdamW, 3 of 512 for SGDM per CU), against the C oracle on
+    sampled chunks."""
+    import sr_states
+    from conftest import assert_bits_or_nan
+
+    from oracle import c_oracle, sr_oracle
+
+    n = (1 << 16) * block_size * 4 + 9
+    gen = torch.Generator(device=cuda).manual_seed(block_size)
+    p = torch.nn.Parameter(torch.empty(n, device=cuda).normal_(std=0.02, generator=gen))
+    p.grad = torch.empty(n, device=cuda).normal_(std=1e-3, generator=gen)
+    starts = [0, n // 2 + 11, n - CHUNK]
+    before = {s: (p.detach()[s:s + CHUNK].cpu(), p.grad[s:s + CHUNK].cpu()) for s in starts}
+    if kind == "adamw":
+        formats = ((torch.bfloat16, "stochastic"),) * 2
+        opt = sr_states.AdamWHip([p], lr=3e-4, weight_decay=0.01, seed=5, block_size=block_size)
+        names = ("exp_avg", "exp_avg_sq")
+    else:
+        formats = ((torch.float16, "stochastic"),)
+        opt = sr_states.SGDMHip([p], lr=0.1, momentum=0.9, seed=5, block_size=block_size,
+                                state_format=sr_states.StateFormat(torch.float16))
+        names = ("momentum_buffer",)
+    opt.step()
+    torch.cuda.synchronize()
+    key = sr_oracle.update_key(5, 1, 0)
+    for start, (p_ref, g_ref) in before.items():
+        refs = [torch.zeros(CHUNK, dtype=d) for d, _ in formats]
+        if kind == "adamw":
+            c_oracle.adamw_step_(p_ref, g_ref, *refs, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01,
+                                 step=1, formats=formats, seed=key, offset=start)
+        else:
+            c_oracle.sgdm_step_(p_ref, g_ref, *refs, lr=0.1, momentum_factor=0.9, formats=formats, seed=key,
+                                offset=start)
+        sl = slice(start, start + CHUNK)
+        assert_bits_or_nan(p.detach()[sl].cpu(), p_ref, f"{kind}/{block_size} parameter at {start}")
+        for name, ref in zip(names, refs):
+            assert_bits_or_nan(opt.state[p][name][sl].cpu(), ref, f"{kind}/{block_size} {name} at {start}")
