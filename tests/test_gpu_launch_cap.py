@@ -8,7 +8,8 @@ and gradient, BF16 stochastic moments) on one tensor of 2^28 elements
 (5.4 GB) with the rule's cap and with none, interleaved over three rounds:
 the occupancy calculator must report the rule's 8 workgroups per CU, and
 the capped kernel must be at least as fast as the uncapped one (on MI355X
-it is 3-4% faster at this footprint).  The single-tensor entries and the
+it is 3-4% faster at this footprint).  The single-tensor entries, AdamW
+with two stochastic FP16 or FP8 moments (96 KiB in flight) and the
 optimizers at 256-, 512- and 1024-lane workgroups, capped past 2^16 tiles,
 are held to the C oracle.
 """
@@ -96,6 +97,38 @@ def test_capped_single_tensor_launches_equal_the_oracle(cuda, kind):
         assert_bits_or_nan(p[sl].cpu(), p_ref, f"{kind} parameter at {start}")
         for k, (state, ref) in enumerate(zip(states, refs)):
             assert_bits_or_nan(state[sl].cpu(), ref, f"{kind} state {k} at {start}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float8_e4m3fn, torch.float8_e5m2],
+                         ids=lambda d: str(d).replace("torch.", ""))
+def test_capped_launches_with_two_minifloat_sr_moments_equal_the_oracle(cuda, dtype):
+    """AdamW with both moments stochastic FP16 or FP8 keeps 96 KiB in flight (10 or 12 workgroups
+    per CU); past 2^16 tiles, sampled chunks against the C oracle."""
+    import sr_states
+    from conftest import assert_bits_or_nan
+
+    from oracle import c_oracle, sr_oracle
+
+    n = (1 << 25) + 517
+    gen = torch.Generator(device=cuda).manual_seed(29)
+    p = torch.nn.Parameter(torch.empty(n, device=cuda).normal_(std=0.02, generator=gen))
+    p.grad = torch.empty(n, device=cuda).normal_(std=1e-3, generator=gen)
+    starts = [0, n // 2 + 5, n - CHUNK]
+    before = {s: (p.detach()[s:s + CHUNK].cpu(), p.grad[s:s + CHUNK].cpu()) for s in starts}
+    formats = ((dtype, "stochastic"),) * 2
+    opt = sr_states.AdamWHip([p], lr=3e-4, weight_decay=0.01, seed=13,
+                             state_format=sr_states.StateFormat(dtype, "stochastic"))
+    opt.step()
+    torch.cuda.synchronize()
+    key = sr_oracle.update_key(13, 1, 0)
+    for start, (p_ref, g_ref) in before.items():
+        refs = [torch.zeros(CHUNK, dtype=dtype) for _ in range(2)]
+        c_oracle.adamw_step_(p_ref, g_ref, *refs, lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01,
+                             step=1, formats=formats, seed=key, offset=start)
+        sl = slice(start, start + CHUNK)
+        assert_bits_or_nan(p.detach()[sl].cpu(), p_ref, f"{dtype} parameter at {start}")
+        for name, ref in zip(("exp_avg", "exp_avg_sq"), refs):
+            assert_bits_or_nan(opt.state[p][name][sl].cpu(), ref, f"{dtype} {name} at {start}")
 
 
 @pytest.mark.parametrize("kind, block_size", [("adamw", 256), ("adamw", 1024), ("sgdm", 512)])
