@@ -54,6 +54,10 @@ timed workload's tensors, read before the first step and after the last,
 replayed through every step (warmup and both timed passes) by the C oracle
 and compared byte for byte; the run fails if any byte differs.
 
+``config.resident_cap`` is the resident-workgroup cap the library's large
+optimizer launches ran with: "rule" (its own choice per launch), or the value
+of ``SR_STATES_RESIDENT_CAP`` when that environment variable replaces it.
+
 ``--workload cast_sizes`` times the reference cast benchmark's size sweep
 (2^10 to 2^24): this backend's stochastic and nearest BF16 casts and torch's
 conversion, per size.
@@ -1073,6 +1077,7 @@ def main():
             "grad_dtype": str(spec["g_dtype"]).replace("torch.", ""),
             "state_formats": [f"{str(d).replace('torch.', '')}/{r}" for d, r in spec["formats"]],
             "bytes_per_element": bpe,
+            "resident_cap": os.environ.get("SR_STATES_RESIDENT_CAP") or "rule",
             "parallelism": "single GPU",
         },
         "roofline": {

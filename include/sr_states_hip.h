@@ -21,8 +21,11 @@
  *     dynamic LDS that their kernels never touch, to keep about 80 KiB of
  *     tiles in flight per CU (96 KiB for AdamW with two FP16/FP8
  *     stochastic moments); kernels of other streams running beside such a
- *     launch find that LDS taken on the CUs it occupies.  Results do not
- *     depend on it.
+ *     launch find that LDS taken on the CUs it occupies.  The environment
+ *     variable SR_STATES_RESIDENT_CAP=k (0-16, read once per process)
+ *     replaces that rule for every optimizer launch of 2^16 tiles or more:
+ *     at most k workgroups per CU, none reserved for k = 0.  Results do
+ *     not depend on either.
  */
 #ifndef SR_STATES_HIP_H
 #define SR_STATES_HIP_H

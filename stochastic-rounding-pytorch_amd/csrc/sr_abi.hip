@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <mutex>
 #include <string>
@@ -97,11 +98,19 @@ int launch(const void* fn, int block, uint32_t tiles, void* arg, void* stream, u
   return SR_OK;
 }
 
+// SR_STATES_RESIDENT_CAP, read once (sr::resident_cap_override): the cap of
+// every launch of at least 2^16 tiles, or -1 for the rule.
+int cap_override() {
+  static const int value = sr::resident_cap_override(std::getenv("SR_STATES_RESIDENT_CAP"));
+  return value;
+}
+
 // Whether an encoding rounds stochastically to FP16 or FP8.
 bool minifloat_sr(int enc) { return enc == sr::ENC_F16_SR || enc == sr::ENC_E4M3_SR || enc == sr::ENC_E5M2_SR; }
 
 // Resident-workgroup cap of an AdamW launch (sr::resident_cap).
 uint32_t adamw_cap(int pi, int gi, int me, int ve, int block, uint32_t tiles) {
+  if (cap_override() >= 0) return tiles >= sr::kResidentCapMinTiles ? static_cast<uint32_t>(cap_override()) : 0u;
   const int bytes = 2 * sr::enc_bytes(param_enc(pi)) + sr::enc_bytes(param_enc(gi)) + 2 * sr::enc_bytes(me) +
                     2 * sr::enc_bytes(ve);
   const uint32_t in_flight = minifloat_sr(me) && minifloat_sr(ve) ? sr::kInFlightBytesPerCuTwoMinifloatSr
@@ -113,6 +122,7 @@ uint32_t adamw_cap(int pi, int gi, int me, int ve, int block, uint32_t tiles) {
 
 // Resident-workgroup cap of a momentum-SGD launch.
 uint32_t sgdm_cap(int pi, int gi, int ue, int block, uint32_t tiles) {
+  if (cap_override() >= 0) return tiles >= sr::kResidentCapMinTiles ? static_cast<uint32_t>(cap_override()) : 0u;
   const int bytes = 2 * sr::enc_bytes(param_enc(pi)) + sr::enc_bytes(param_enc(gi)) + 2 * sr::enc_bytes(ue);
   return sr::resident_cap(tiles, static_cast<uint32_t>(block),
                           static_cast<uint32_t>(sr::lane_elements(param_enc(pi), param_enc(gi), ue, ue)),

@@ -18,6 +18,7 @@ namespace sr {
 
 constexpr uint32_t kLdsPerCu = 160u * 1024u;  // gfx950
 constexpr int kCapMaxBlock = 1024;
+constexpr uint32_t kCapLdsMax = static_cast<uint32_t>(kResidentCapOverrideMax);
 
 // Dynamic LDS per workgroup that leaves at most `cap` workgroups of `block`
 // lanes resident per CU; 0 for cap 0.  The kernels it serves use no LDS, so
@@ -31,8 +32,8 @@ constexpr int kCapMaxBlock = 1024;
 // runs uncapped, and the failure is cleared from the runtime's last error so
 // that no later, unrelated error check reports it.
 inline size_t cap_lds(const void* fn, int block, uint32_t cap) {
-  static std::atomic<uint32_t> known[kCapMaxBlock / 64][kResidentCapMax + 1];
-  if (cap == 0 || cap > kResidentCapMax || block < 64 || block > kCapMaxBlock || block % 64) return 0;
+  static std::atomic<uint32_t> known[kCapMaxBlock / 64][kCapLdsMax + 1];
+  if (cap == 0 || cap > kCapLdsMax || block < 64 || block > kCapMaxBlock || block % 64) return 0;
   std::atomic<uint32_t>& slot = known[block / 64 - 1][cap];
   const uint32_t kept = slot.load(std::memory_order_relaxed);
   if (kept != 0) return static_cast<size_t>(kept - 1) * 256;

@@ -116,4 +116,24 @@ SR_HOST_DEVICE inline uint32_t resident_cap(uint32_t tiles, uint32_t block, uint
   return cap >= 1 && cap <= kResidentCapMax ? static_cast<uint32_t>(cap) : 0u;
 }
 
+// The environment can replace the rule: SR_STATES_RESIDENT_CAP=k caps every
+// optimizer launch of at least 2^16 tiles (any parameter dtype) at k
+// workgroups per CU, 1 <= k <= kResidentCapOverrideMax, and 0 leaves them
+// all uncapped.  For measuring the rule and for workloads whose best cap
+// differs; results never depend on it.  resident_cap_override parses the
+// variable's text: the override, or -1 for "use the rule" (unset, empty or
+// not a number in range).
+constexpr int kResidentCapOverrideMax = 16;
+
+inline int resident_cap_override(const char* text) {
+  if (text == nullptr || *text == '\0') return -1;
+  int value = 0;
+  for (const char* c = text; *c; ++c) {
+    if (*c < '0' || *c > '9') return -1;
+    value = value * 10 + (*c - '0');
+    if (value > kResidentCapOverrideMax) return -1;
+  }
+  return value;
+}
+
 }  // namespace sr

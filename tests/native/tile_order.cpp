@@ -6,7 +6,8 @@
 // checks launch_shape: one row when the padded grid fits the per-dimension
 // work-item limit, otherwise rows of whole chunk rounds whose workgroups,
 // numbered row by row, still cover each tile exactly once.  Finally it pins
-// resident_cap, the resident-workgroup cap of large optimizer launches.
+// resident_cap, the resident-workgroup cap of large optimizer launches, and
+// resident_cap_override, the parse of its environment override.
 #include <cstdint>
 #include <cstdio>
 #include <vector>
@@ -143,6 +144,17 @@ int main() {
     const uint32_t got = sr::resident_cap(3022848u, 128u, 4, c.bytes, true, sr::kInFlightBytesPerCuTwoMinifloatSr);
     if (got != c.want) {
       std::printf("resident_cap(96 KiB, %u B) = %u, expected %u\n", c.bytes, got, c.want);
+      ++failures;
+    }
+  }
+  // resident_cap_override: the text of SR_STATES_RESIDENT_CAP, -1 = the rule.
+  struct Override { const char* text; int want; };
+  for (const Override& c : {Override{nullptr, -1}, Override{"", -1}, Override{"0", 0}, Override{"8", 8},
+                            Override{"16", 16}, Override{"017", -1}, Override{"17", -1}, Override{"-1", -1},
+                            Override{"8 ", -1}, Override{"x", -1}, Override{"99999999999", -1}}) {
+    const int got = sr::resident_cap_override(c.text);
+    if (got != c.want) {
+      std::printf("resident_cap_override(%s) = %d, expected %d\n", c.text ? c.text : "null", got, c.want);
       ++failures;
     }
   }

@@ -11,13 +11,18 @@ the capped kernel must be at least as fast as the uncapped one (on MI355X
 it is 3-4% faster at this footprint).  The single-tensor entries, AdamW
 with two stochastic FP16 or FP8 moments (96 KiB in flight) and the
 optimizers at 256-, 512- and 1024-lane workgroups, capped past 2^16 tiles,
-are held to the C oracle.
+are held to the C oracle.  SR_STATES_RESIDENT_CAP, which replaces the
+rule for a process, changes the time of a launch and none of its bytes.
 """
 
 from __future__ import annotations
 
 import ctypes
+import json
+import os
 import statistics
+import subprocess
+import sys
 from pathlib import Path
 
 import pytest
@@ -171,3 +176,60 @@ def test_capped_launches_of_other_workgroup_sizes_equal_the_oracle(cuda, kind, b
         assert_bits_or_nan(p.detach()[sl].cpu(), p_ref, f"{kind}/{block_size} parameter at {start}")
         for name, ref in zip(names, refs):
             assert_bits_or_nan(opt.state[p][name][sl].cpu(), ref, f"{kind}/{block_size} {name} at {start}")
+
+
+# One process per setting of SR_STATES_RESIDENT_CAP (the library reads it
+# once): two AdamW steps on 2^25 + 3 elements (65537 tiles, so capped), a
+# digest of the parameter and moments, then the mean time of 30 launches.
+_OVERRIDE_CHILD = """
+import hashlib, json, torch
+import sr_states
+dev = torch.device("cuda", 0)
+n = (1 << 25) + 3
+gen = torch.Generator(device=dev).manual_seed(31)
+p = torch.empty(n, device=dev).normal_(std=0.02, generator=gen)
+g = torch.empty(n, device=dev).normal_(std=1e-3, generator=gen)
+m = torch.zeros(n, device=dev, dtype=torch.bfloat16)
+v = torch.zeros(n, device=dev, dtype=torch.bfloat16)
+fmt = (sr_states.StateFormat(torch.bfloat16, "stochastic"),) * 2
+hyper = dict(lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, seed=0x5EED, formats=fmt)
+for step in (1, 2):
+    sr_states.hip_adamw_step_(p, g, m, v, step=step, **hyper)
+torch.cuda.synchronize()
+digest = hashlib.sha256()
+for t in (p, m, v):
+    digest.update(t.view(torch.uint8).cpu().numpy().tobytes())
+for _ in range(5):
+    sr_states.hip_adamw_step_(p, g, m, v, step=3, **hyper)
+a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+a.record()
+for _ in range(30):
+    sr_states.hip_adamw_step_(p, g, m, v, step=3, **hyper)
+b.record()
+b.synchronize()
+print(json.dumps({"digest": digest.hexdigest(), "ms": a.elapsed_time(b) / 30}), flush=True)
+"""
+
+
+def test_resident_cap_override_changes_time_not_bytes(cuda):
+    """SR_STATES_RESIDENT_CAP=0 (uncapped) and =1 give the same bytes as the rule's cap of 8, and
+    cap 1 (two waves per CU) is far slower, so the variable does reach the launches."""
+    root = Path(__file__).resolve().parents[1]
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join(
+        [str(root), str(root / "stochastic-rounding-pytorch_amd"), env.get("PYTHONPATH", "")])
+    runs = {}
+    for setting in ("rule", "0", "1"):
+        if setting == "rule":
+            env.pop("SR_STATES_RESIDENT_CAP", None)
+        else:
+            env["SR_STATES_RESIDENT_CAP"] = setting
+        print(f"child with SR_STATES_RESIDENT_CAP={setting}", flush=True)
+        done = subprocess.run([sys.executable, "-c", _OVERRIDE_CHILD], env=env, capture_output=True, text=True,
+                              timeout=100)
+        assert done.returncode == 0, f"{setting}: exit {done.returncode}\n{done.stderr[-2000:]}"
+        runs[setting] = json.loads(done.stdout.strip().splitlines()[-1])
+    assert runs["0"]["digest"] == runs["rule"]["digest"]
+    assert runs["1"]["digest"] == runs["rule"]["digest"]
+    times = {k: round(r["ms"], 4) for k, r in runs.items()}
+    assert runs["1"]["ms"] > 1.5 * runs["rule"]["ms"], times
