@@ -113,8 +113,7 @@ uint32_t adamw_cap(int pi, int gi, int me, int ve, int block, uint32_t tiles) {
   if (cap_override() >= 0) return tiles >= sr::kResidentCapMinTiles ? static_cast<uint32_t>(cap_override()) : 0u;
   const int bytes = 2 * sr::enc_bytes(param_enc(pi)) + sr::enc_bytes(param_enc(gi)) + 2 * sr::enc_bytes(me) +
                     2 * sr::enc_bytes(ve);
-  const uint32_t in_flight = minifloat_sr(me) && minifloat_sr(ve) ? sr::kInFlightBytesPerCuTwoMinifloatSr
-                                                                  : sr::kInFlightBytesPerCu;
+  const uint32_t in_flight = sr::adamw_in_flight(gi == 1, minifloat_sr(me) && minifloat_sr(ve));
   return sr::resident_cap(tiles, static_cast<uint32_t>(block),
                           static_cast<uint32_t>(sr::lane_elements(param_enc(pi), param_enc(gi), me, ve)),
                           static_cast<uint32_t>(bytes), pi == 0, in_flight);
@@ -126,7 +125,7 @@ uint32_t sgdm_cap(int pi, int gi, int ue, int block, uint32_t tiles) {
   const int bytes = 2 * sr::enc_bytes(param_enc(pi)) + sr::enc_bytes(param_enc(gi)) + 2 * sr::enc_bytes(ue);
   return sr::resident_cap(tiles, static_cast<uint32_t>(block),
                           static_cast<uint32_t>(sr::lane_elements(param_enc(pi), param_enc(gi), ue, ue)),
-                          static_cast<uint32_t>(bytes), pi == 0);
+                          static_cast<uint32_t>(bytes), pi == 0, sr::sgdm_in_flight(ue == sr::ENC_F16_SR));
 }
 
 // Tiles of block * lanes elements covering n elements, or fail if they do

@@ -78,37 +78,60 @@ SR_HOST_DEVICE inline LaunchShape launch_shape(uint32_t tiles, uint32_t block,
 // Resident workgroups per CU of a large optimizer launch.  The fused updates
 // use few registers, so 16 of their 128-lane workgroups fit on a CU, and
 // that many keep more memory requests in flight than HBM can serve: the
-// surplus only adds contention.  Measured on MI355X (every cap exact,
-// interleaved in one process, through the library's multi-tensor launches),
-// the rate peaks with about 80 KiB of tiles in flight per CU, i.e. cap =
-// round(80 KiB / tile bytes):
-//   north star (FP32 p/g, BF16-SR m/v, 20 B):  6.21 -> 6.40 TB/s at 8
-//   2^26-element tensor, same streams:           6.45 -> 6.71 at 8
-//   E4M3-SR m + BF16-SR v (18 B): 6.20 -> 6.38 at 9
-//   SGDM, FP16-SR momentum (16 B): 6.31 -> 6.44 at the rule's 10 (6.53 at 9)
-//   FP32 moments (28 B): 6.03 -> 6.18-6.26 at the rule's 6 (6.24 at 7)
-// AdamW launches whose two moments both round stochastically to FP16 or FP8
-// spend longer in each workgroup's arithmetic (two minifloat encoders per
-// element) and peak nearer 96 KiB: FP16-SR m/v (20 B) 6.18 -> 6.33 at 10
-// (6.20 at 8), E4M3-SR m/v (16 B) 6.22 -> 6.35 at 12 (6.25 at 10), E5M2-SR
-// m/v 6.28 -> 6.34 at 12 (6.22 at 10).
+// surplus only adds contention.  The cap is round(budget / tile bytes), the
+// budget being the bytes of tiles in flight per CU at which the rate peaked
+// on MI355X.  Every cap exact, each launch family swept through the
+// library's own launches (SR_STATES_RESIDENT_CAP, two runs per cap), TB/s
+// uncapped -> at the cap:
+//   AdamW, FP32 gradients: 80 KiB.  North star (FP32 p/g, BF16-SR m/v,
+//     20 B) 6.22 -> 6.42 at 8; one 2^26-element tensor 6.46 -> 6.64 at 8;
+//     E4M3-SR m + BF16-SR v (18 B) 6.22 -> 6.41 at 9; FP32 moments (28 B)
+//     6.01 -> 6.23 at 6; BF16-, FP16- and FP8-nearest moments peak at 8,
+//     8 and 10.
+//   AdamW, BF16 gradients (GPT-2 shapes): 96 KiB.  BF16-SR m/v (18 B)
+//     6.29 -> 6.36 at 11, 6.27 at 80 KiB's 9 (on another machine 6.34 at
+//     9, 6.40 at 11); BF16-RN, FP16-RN and FP32 moments also peak at 11,
+//     11 and 7.
+//   AdamW whose two moments both round stochastically to FP16 or FP8 (two
+//     minifloat encoders per element lengthen each workgroup's life): 96 KiB
+//     with FP32 gradients (FP16-SR m/v 6.20 -> 6.32 at 10, E4M3-SR and
+//     E5M2-SR 6.23 -> 6.28 at 12); with BF16 gradients none at all (FP16-SR
+//     6.31 uncapped, 6.22 at 11; FP8-SR 6.36-6.39 uncapped, 5.97 at 12).
+//   SGDM: 88 KiB (BF16-SR, BF16-RN and FP16-RN momentum, 16 B: 6.36-6.38 ->
+//     6.47-6.49 at 11; FP32: 6.21 -> 6.43 at 9; FP8: best at 12-13), except
+//     FP16-SR momentum at 72 KiB (6.35-6.38 -> 6.58-6.61 at 9, against
+//     6.50-6.54 at 10 and 6.48 at 11, on three machines).
 // Launches with BF16 parameters spend more of a workgroup's life in
 // arithmetic; caps of 11 to 15 moved them by under 1%, so they stay
 // uncapped, as do launches of fewer than 2^16 tiles (2^25 elements at 128
 // lanes), whose tail the cap lengthens (2^24 elements: 6.50 -> 6.46;
-// 2^25: 6.53 -> 6.62), and the casts (every cap slower).
-constexpr uint32_t kInFlightBytesPerCu = 80u * 1024u;
-constexpr uint32_t kInFlightBytesPerCuTwoMinifloatSr = 96u * 1024u;
+// 2^25: 6.53 -> 6.62), and the casts (every cap slower).  A budget that
+// rounds to more than kResidentCapMax workgroups also means no cap.
+constexpr uint32_t kInFlightAdamW = 80u * 1024u;
+constexpr uint32_t kInFlightAdamWWide = 96u * 1024u;
+constexpr uint32_t kInFlightSgdm = 88u * 1024u;
+constexpr uint32_t kInFlightSgdmF16Sr = 72u * 1024u;
 constexpr uint32_t kResidentCapMinTiles = 1u << 16;
-constexpr uint32_t kResidentCapMax = 12;
+constexpr uint32_t kResidentCapMax = 14;
+
+// In-flight budget of an AdamW launch with FP32 parameters, or 0 for no cap.
+SR_HOST_DEVICE constexpr uint32_t adamw_in_flight(bool bf16_gradient, bool two_minifloat_sr) {
+  return bf16_gradient ? (two_minifloat_sr ? 0u : kInFlightAdamWWide)
+                       : (two_minifloat_sr ? kInFlightAdamWWide : kInFlightAdamW);
+}
+
+// In-flight budget of a momentum-SGD launch with FP32 parameters.
+SR_HOST_DEVICE constexpr uint32_t sgdm_in_flight(bool f16_sr_momentum) {
+  return f16_sr_momentum ? kInFlightSgdmF16Sr : kInFlightSgdm;
+}
 
 // Workgroups per CU to leave resident for an optimizer launch of `tiles`
 // tiles of `block` lanes times `lanes` elements, moving `bytes_per_element`
 // bytes per element with `in_flight` bytes of tiles in flight per CU, or 0
-// for no cap.
+// for no cap (also for in_flight 0).
 SR_HOST_DEVICE inline uint32_t resident_cap(uint32_t tiles, uint32_t block, uint32_t lanes,
                                             uint32_t bytes_per_element, bool fp32_params,
-                                            uint32_t in_flight = kInFlightBytesPerCu) {
+                                            uint32_t in_flight = kInFlightAdamW) {
   if (!fp32_params || tiles < kResidentCapMinTiles) return 0;
   const uint64_t tile_bytes = static_cast<uint64_t>(block) * lanes * bytes_per_element;
   if (tile_bytes == 0) return 0;

@@ -237,8 +237,9 @@ __global__ void fill_update_inputs(float* p, float* g, uint64_t n) {
 // a parameter of p_bytes, a gradient of g_bytes and states of m_bytes and
 // v_bytes per element (v_bytes 0: one state), over `reps` launches after two
 // untimed ones, at the best of the placements kCeilingGaps and of three
-// launch policies: no resident-workgroup cap, the library's cap for this
-// pattern (sr::resident_cap) and half of it.  (With no arithmetic to wait
+// launch policies: no resident-workgroup cap, the cap of an 80 KiB budget
+// for this pattern (sr::resident_cap, the library's for FP32 gradients) and
+// half of it.  (With no arithmetic to wait
 // for, the trivial kernel's workgroups are short-lived and it keeps enough
 // bytes in flight with fewer of them: the north star's streams at 31 GB ran
 // at 6.18 TB/s uncapped, 6.31 at 8 per CU and 6.38 at 4.)  Supported
@@ -330,7 +331,7 @@ extern "C" int sr_cast_ceiling(uint64_t n, int out_bytes, int buffers, int reps,
 // library's fused AdamW kernel (ms_fused[i]) over one FP32 parameter and
 // gradient and two BF16 moments of n elements (20 bytes per element), at
 // resident-workgroup cap caps[i]: -1 for the library's rule
-// (sr::resident_cap), 0 for none, 1-12 for that many workgroups per CU;
+// (sr::resident_cap), 0 for none, 1-16 for that many workgroups per CU;
 // resident[i] receives the workgroups per CU the fused launch allowed (the
 // runtime's occupancy calculator).  Each is averaged over `reps` launches
 // after two untimed ones; the two kernels alternate cap by cap.  n must be a
@@ -341,7 +342,7 @@ extern "C" int sr_launch_cap_sweep(uint64_t n, int reps, const int* caps, int nc
                                    float* ms_fused, int* resident) {
   if (!valid_streams(n, reps) || !caps || ncaps < 1 || ncaps > 32 || !ms_trivial || !ms_fused || !resident) return 1;
   for (int i = 0; i < ncaps; ++i)
-    if (caps[i] < -1 || caps[i] > static_cast<int>(sr::kResidentCapMax)) return 1;
+    if (caps[i] < -1 || caps[i] > sr::kResidentCapOverrideMax) return 1;
   const uint32_t tiles = static_cast<uint32_t>(n / kTile);
   const sr::LaunchShape shape = sr::launch_shape(tiles, kBlock);
   auto fused = sr::adamw_kernel<sr::ENC_F32, sr::ENC_F32, sr::ENC_BF16_SR, sr::ENC_BF16_SR>;

@@ -113,7 +113,7 @@ int main() {
     }
   }
   // resident_cap: round(in-flight bytes / tile bytes) for FP32-parameter
-  // launches of at least 2^16 tiles, when that is 1..12; otherwise none (0).
+  // launches of at least 2^16 tiles, when that is 1..14; otherwise none (0).
   struct Cap { uint32_t tiles, block, bytes; bool fp32; uint32_t want; };
   for (const Cap& c : {Cap{3022848u, 128u, 20u, true, 8u},   // north star: 80 KiB / 10 KiB
                        Cap{65536u, 128u, 20u, true, 8u},     // smallest capped launch
@@ -125,7 +125,8 @@ int main() {
                        Cap{3022848u, 128u, 24u, true, 7u},   // 6.67
                        Cap{3022848u, 128u, 14u, true, 11u},  // 11.43
                        Cap{3022848u, 128u, 13u, true, 12u},  // 12.31
-                       Cap{3022848u, 128u, 12u, true, 0u},   // 13.33: above the largest cap
+                       Cap{3022848u, 128u, 12u, true, 13u},  // 13.33
+                       Cap{3022848u, 128u, 11u, true, 0u},   // 14.55 rounds to 15: above the largest cap
                        Cap{3022848u, 256u, 20u, true, 4u},
                        Cap{3022848u, 1024u, 20u, true, 1u},
                        Cap{3022848u, 1024u, 40u, true, 1u},  // 0.5 rounds up
@@ -138,12 +139,29 @@ int main() {
       ++failures;
     }
   }
-  // 96 KiB in flight (AdamW with two stochastic FP16/FP8 moments).
-  struct Cap96 { uint32_t bytes, want; };
-  for (const Cap96& c : {Cap96{20u, 10u}, Cap96{16u, 12u}, Cap96{18u, 11u}, Cap96{28u, 7u}, Cap96{15u, 0u}}) {
-    const uint32_t got = sr::resident_cap(3022848u, 128u, 4, c.bytes, true, sr::kInFlightBytesPerCuTwoMinifloatSr);
+  // The budgets by launch family, and the caps they give at 128 lanes.
+  if (sr::adamw_in_flight(false, false) != 80u * 1024u || sr::adamw_in_flight(false, true) != 96u * 1024u ||
+      sr::adamw_in_flight(true, false) != 96u * 1024u || sr::adamw_in_flight(true, true) != 0u ||
+      sr::sgdm_in_flight(false) != 88u * 1024u || sr::sgdm_in_flight(true) != 72u * 1024u) {
+    std::printf("in-flight budgets differ from 80/96/96/0 and 88/72 KiB\n");
+    ++failures;
+  }
+  struct Budget { uint32_t in_flight, bytes, want; };
+  for (const Budget& c : {Budget{96u * 1024u, 20u, 10u},  // AdamW, two FP16-SR moments
+                          Budget{96u * 1024u, 16u, 12u},  // two FP8-SR moments
+                          Budget{96u * 1024u, 18u, 11u},  // BF16 gradient, BF16 moments (10.67)
+                          Budget{96u * 1024u, 26u, 7u},   // BF16 gradient, FP32 moments (7.38)
+                          Budget{96u * 1024u, 15u, 13u},  // 12.8
+                          Budget{96u * 1024u, 14u, 14u},  // 13.71
+                          Budget{96u * 1024u, 13u, 0u},   // 14.77 rounds to 15
+                          Budget{0u, 18u, 0u},            // no budget: no cap
+                          Budget{88u * 1024u, 16u, 11u},  // SGDM, 2-byte momentum
+                          Budget{88u * 1024u, 20u, 9u},   // SGDM, FP32 momentum (8.8)
+                          Budget{88u * 1024u, 14u, 13u},  // SGDM, FP8 momentum (12.57)
+                          Budget{72u * 1024u, 16u, 9u}}) {  // SGDM, FP16-SR momentum
+    const uint32_t got = sr::resident_cap(3022848u, 128u, 4, c.bytes, true, c.in_flight);
     if (got != c.want) {
-      std::printf("resident_cap(96 KiB, %u B) = %u, expected %u\n", c.bytes, got, c.want);
+      std::printf("resident_cap(%u B in flight, %u B) = %u, expected %u\n", c.in_flight, c.bytes, got, c.want);
       ++failures;
     }
   }

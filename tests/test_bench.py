@@ -109,7 +109,7 @@ def test_ceiling_helpers_refuse_bad_arguments_before_any_device_work():
         return lib.sr_launch_cap_sweep(n, reps, (ctypes.c_int * max(len(caps), 1))(*caps), len(caps), *out)
 
     assert sweep(n, [-2]) == 1  # below -1 (the rule)
-    assert sweep(n, [13]) == 1  # above the largest cap
+    assert sweep(n, [17]) == 1  # above the largest cap
     assert sweep(n, []) == 1
     assert sweep(n + 1, [0]) == 1  # not whole tiles
     assert sweep(n, [0], reps=0) == 1
