@@ -31,7 +31,7 @@ the same streams (widths, tile shape and order, non-temporal accesses) over
 the same number of elements (tests/native/stream_ceiling.hip), timed in the
 same process after the workload's tensors are freed, also over
 back-to-back launches, at the best of four stream placements and three
-resident-workgroup caps (none, the library's, half of it): what the memory
+resident-workgroup caps (none, that of an 80 KiB budget, half of it): what the memory
 system gives this access pattern at this footprint.  ``frac`` there is the
 fused kernel's rate over it.
 

@@ -18,10 +18,12 @@
  *   - Counters are 32-bit: every seed/offset/step word is taken modulo 2^32,
  *     exactly as the reference masks them (sr_states/_hash.py:5-50).
  *   - Optimizer launches of 2^16 tiles or more with FP32 parameters reserve
- *     dynamic LDS that their kernels never touch, to keep about 80 KiB of
- *     tiles in flight per CU (96 KiB for AdamW with two FP16/FP8
- *     stochastic moments); kernels of other streams running beside such a
- *     launch find that LDS taken on the CUs it occupies.  The environment
+ *     dynamic LDS that their kernels never touch, to keep a measured budget
+ *     of tiles in flight per CU: AdamW 80 KiB, or 96 KiB with BF16
+ *     gradients or with two FP16/FP8 stochastic moments (none with both);
+ *     SGDM 88 KiB, or 72 KiB with FP16 stochastic momentum.  Kernels of
+ *     other streams running beside such a launch find that LDS taken on the
+ *     CUs it occupies.  The environment
  *     variable SR_STATES_RESIDENT_CAP=k (0-16, read once per process)
  *     replaces that rule for every optimizer launch of 2^16 tiles or more:
  *     at most k workgroups per CU, none reserved for k = 0.  Results do
