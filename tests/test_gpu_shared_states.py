@@ -128,3 +128,25 @@ def test_checkpoint_loads_into_shared_views(cuda):
         assert torch.equal(a.detach().view(torch.int32).cpu(), b.detach().view(torch.int32).cpu())
         for name in opt._state_names:
             assert torch.equal(opt.state[a][name].view(torch.uint8).cpu(), restored.state[b][name].view(torch.uint8).cpu())
+
+
+def test_allocations_split_at_the_limit_give_the_same_bytes(cuda, monkeypatch):
+    """With a 4 KiB limit the group's states spread over several allocations; bytes unchanged."""
+    from sr_states.optim import _state
+
+    monkeypatch.setattr(_state, "_SHARED_MAX_BYTES", 4096)
+    runs = []
+    for shared in (True, False):
+        params, opt = _make(AdamWHip, cuda, shared)
+        for step in range(3):
+            _grads(params, step)
+            opt.step()
+        torch.cuda.synchronize()
+        runs.append((params, opt))
+    (params, opt), (own_params, own_opt) = runs
+    bases = {opt.state[p]["exp_avg"].untyped_storage().data_ptr() for p in params}
+    assert 2 < len(bases) < len(params) + 1
+    for index, (a, b) in enumerate(zip(params, own_params)):
+        assert_bits_or_nan(a.detach().cpu(), b.detach().cpu(), f"parameter {index}")
+        for name in opt._state_names:
+            assert_bits_or_nan(opt.state[a][name].cpu(), own_opt.state[b][name].cpu(), f"{name} {index}")
