@@ -54,6 +54,11 @@ timed workload's tensors, read before the first step and after the last,
 replayed through every step (warmup and both timed passes) by the C oracle
 and compared byte for byte; the run fails if any byte differs.
 
+``--separate-states`` gives every optimizer state an allocation of its own,
+as the reference does, instead of the optimizers' default of one allocation
+per state name for the states a step creates together;
+``config.state_allocation`` says which ran.
+
 ``config.resident_cap`` is the resident-workgroup cap the library's large
 optimizer launches ran with: "rule" (its own choice per launch), or the value
 of ``SR_STATES_RESIDENT_CAP`` when that environment variable replaces it.
@@ -926,6 +931,9 @@ def main():
     parser.add_argument("--no-torch-baseline", action="store_true",
                         help="skip timing torch's fused optimizer with FP32 states on the same tensors")
     parser.add_argument("--cpu-seconds", type=positive_float, default=12.0)
+    parser.add_argument("--separate-states", action="store_true",
+                        help="one allocation per optimizer state, as the reference makes them (default: the "
+                             "states a step creates share one allocation per state name)")
     parser.add_argument("--state-format", default=None, metavar="DTYPE/RULE",
                         help="store every state of the workload in this format instead, e.g. "
                              "float8_e4m3fn/stochastic (the reference's nine policies: "
@@ -992,6 +1000,10 @@ def main():
             "entries": rows}), flush=True)
         return
     work = build(spec, device)
+    if args.separate_states:
+        if work.optimizer is None:
+            raise SystemExit(f"--separate-states does not apply to {args.workload}")
+        work.optimizer._shared_state_allocations = False
     step = work.step
     elements = sum(t.numel() for t in work.tensors)
     # Inputs of the sampled chunks, read before the first step, for the
@@ -1078,6 +1090,8 @@ def main():
             "state_formats": [f"{str(d).replace('torch.', '')}/{r}" for d, r in spec["formats"]],
             "bytes_per_element": bpe,
             "resident_cap": os.environ.get("SR_STATES_RESIDENT_CAP") or "rule",
+            "state_allocation": None if work.optimizer is None else (
+                "separate" if args.separate_states else "shared"),
             "parallelism": "single GPU",
         },
         "roofline": {
