@@ -275,3 +275,36 @@ def test_groups_mixing_dtensor_and_plain_parameters(cuda):
                     assert_bits_or_nan(opt.state[mixed][name], full_opt.state[full][name], f"{name} {k}")
                 _check_oracle(oracle, params, grads, k, 0, mixed.detach(),
                               [opt.state[mixed][name] for name in names], f"rank {rank}, plain parameter {k}")
+
+
+def test_plain_and_dtensor_parameters_share_one_group(cuda):
+    """A group mixing plain parameters and rank 0's shards of DTensor ones: the plain
+    parameters' states share one allocation per name, the DTensor states stay DTensors
+    of their own, and every parameter and state equals the C oracle's update."""
+    params, grads = _problem(cuda, 21)
+    mesh = _mesh((2,), 0)
+    sharded = {1, 4}
+
+    def wrap(index, tensor):
+        return _shard(tensor, mesh, (Shard(0),)) if index in sharded else tensor.clone()
+
+    parameters = [torch.nn.Parameter(wrap(i, p)) for i, p in enumerate(params)]
+    optimizer = sr_states.AdamWHip(parameters, lr=1e-3, weight_decay=0.01, seed=11)
+    for step_grads in grads:
+        for i, (parameter, g) in enumerate(zip(parameters, step_grads)):
+            parameter.grad = wrap(i, g)
+        optimizer.step()
+    torch.cuda.synchronize()
+    names = ("exp_avg", "exp_avg_sq")
+    oracle = _adamw_oracle(11, [(torch.bfloat16, "stochastic")] * 2)
+    plain = [p for i, p in enumerate(parameters) if i not in sharded]
+    for name in names:
+        assert len({optimizer.state[p][name].untyped_storage().data_ptr() for p in plain}) == 1
+    for i, parameter in enumerate(parameters):
+        states = [optimizer.state[parameter][name] for name in names]
+        if i in sharded:
+            assert all(isinstance(s, DTensor) for s in states)
+            _check_oracle(oracle, params, grads, i, shard_start(parameter), parameter.to_local(),
+                          [s.to_local() for s in states], f"DTensor parameter {i}")
+        else:
+            _check_oracle(oracle, params, grads, i, 0, parameter.detach(), states, f"plain parameter {i}")
